@@ -1,0 +1,21 @@
+"""CPU oracle for the MENTAT branching-decode path — TEST INFRASTRUCTURE ONLY.
+
+This package restates, on the CPU, the reference algorithm that the HIP
+library replaces. Every function cites the reference file:line it follows.
+It is the checker, never the thing measured or shipped: only ``tests/``,
+``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``bench.py`` may
+import it. The product path (``mentat_amd``) never imports it.
+
+Modules
+  attention   build_packed_kv gather + per-sequence SDPA decode (fp64 checker
+              and the reference's own torch-CPU path for the CPU baseline)
+  paged_cache BlockAllocator / SequenceState / PagedKVCacheManager bookkeeping
+              (set-based allocator, fork/free, lazy copy-on-write append)
+  sampling    entropy, repetition penalty, gate, argmax/top-K, and the
+              Philox4x32-10 temperature/top-p sampler (C, bit-exact spec)
+  tree        PrefixTree ordering and the generator step decisions
+
+How each function is pinned (golden vectors, closed forms, library routines,
+invariants) is listed in the module docstrings and exercised by
+tests/test_oracle_*.py.
+"""

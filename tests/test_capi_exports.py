@@ -1,0 +1,37 @@
+"""The C-ABI library loads and exports every symbol its header declares (CPU only)."""
+import ctypes
+import os
+
+from mentat_amd import _lib
+
+
+def test_library_is_built():
+    assert os.path.exists(_lib.LIB_PATH), "run python -m mentat_amd.build first"
+
+
+def test_exports_every_declared_symbol():
+    lib = _lib.get_lib()
+    declared = _lib.declared_symbols()
+    assert declared, "no declarations parsed from include/mentat_capi.h"
+    missing = [n for n in declared if not hasattr(lib, n)]
+    assert not missing, f"declared but not exported: {missing}"
+
+
+def test_every_declared_symbol_has_a_ctypes_signature():
+    declared = set(_lib.declared_symbols())
+    assert declared == set(_lib.SIGNATURES), (
+        f"header-only: {sorted(declared - set(_lib.SIGNATURES))}, "
+        f"binding-only: {sorted(set(_lib.SIGNATURES) - declared)}"
+    )
+
+
+def test_abi_version_and_pure_host_queries():
+    lib = _lib.get_lib()
+    assert lib.mentat_abi_version() >= 1
+    # Pure host arithmetic: no device needed.
+    assert lib.mentat_paged_decode_workspace_bytes(0, 32, 8, 128, 16, 4096, 0) == 0
+    nb = lib.mentat_paged_decode_workspace_bytes(64, 32, 8, 128, 16, 4096, 256)
+    assert nb == 64 * 32 * 16 * (128 + 2) * 4
+    c = lib.mentat_paged_decode_auto_chunk(64, 8, 16, 4096)
+    assert c % 16 == 0 and 16 <= c <= 4096
+    assert isinstance(lib.mentat_paged_decode, ctypes._CFuncPtr)

@@ -1,0 +1,104 @@
+"""Pins the attention oracle (CPU): closed forms, GQA mapping, torch SDPA fp64."""
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle.attention import (
+    gather_packed_kv,
+    paged_decode_f64,
+    reference_cpu_decode,
+    sdpa_decode_f64,
+)
+
+
+def _random_paged(rng, N, Hq, Hkv, D, B, lens, num_blocks):
+    perm = rng.permutation(num_blocks)
+    tables, off = [], 0
+    for n in lens:
+        npg = (n + B - 1) // B
+        tables.append(perm[off:off + npg].tolist())
+        off += npg
+    k_pool = rng.standard_normal((num_blocks, B, Hkv, D))
+    v_pool = rng.standard_normal((num_blocks, B, Hkv, D))
+    q = rng.standard_normal((N, Hq, D))
+    return q, k_pool, v_pool, tables
+
+
+def test_gather_layout_matches_table_order():
+    B, Hkv, D = 4, 1, 2
+    pool = np.arange(6 * B * Hkv * D, dtype=np.float64).reshape(6, B, Hkv, D)
+    pk, pv, cu, mx = gather_packed_kv(pool, pool, [[5, 2], [1]], [6, 3], B)
+    assert cu.tolist() == [0, 6, 9] and mx == 6
+    expect_rows = [(5, 0), (5, 1), (5, 2), (5, 3), (2, 0), (2, 1), (1, 0), (1, 1), (1, 2)]
+    for r, (b, s) in enumerate(expect_rows):
+        np.testing.assert_array_equal(pk[r], pool[b, s])
+
+
+def test_empty_batch_gather():
+    pool = np.zeros((2, 4, 1, 2))
+    pk, pv, cu, mx = gather_packed_kv(pool, pool, [], [], 4)
+    assert pk.shape[0] == 0 and cu.tolist() == [0] and mx == 0
+
+
+def test_single_token_returns_v():
+    rng = np.random.default_rng(1)
+    q = rng.standard_normal((1, 4, 8))
+    k = rng.standard_normal((1, 2, 8))
+    v = rng.standard_normal((1, 2, 8))
+    o = sdpa_decode_f64(q, k, v, np.array([0, 1]))
+    for h in range(4):
+        np.testing.assert_allclose(o[0, h], v[0, h // 2], rtol=0, atol=1e-15)
+
+
+def test_identical_keys_give_mean_of_values():
+    rng = np.random.default_rng(2)
+    L = 37
+    k = np.repeat(rng.standard_normal((1, 1, 16)), L, axis=0)
+    v = rng.standard_normal((L, 1, 16))
+    q = rng.standard_normal((1, 3, 16))
+    o = sdpa_decode_f64(q, k, v, np.array([0, L]))
+    np.testing.assert_allclose(o[0], np.broadcast_to(v[:, 0].mean(0), (3, 16)), atol=1e-12)
+
+
+def test_gqa_head_mapping():
+    # Each kv head has a distinct constant value vector; q head h must read kv head h // G.
+    Hq, Hkv, D, L = 8, 2, 4, 5
+    k = np.zeros((L, Hkv, D))
+    v = np.zeros((L, Hkv, D))
+    v[:, 0] = 1.0
+    v[:, 1] = 2.0
+    q = np.ones((1, Hq, D))
+    o = sdpa_decode_f64(q, k, v, np.array([0, L]))
+    np.testing.assert_allclose(o[0, :4], 1.0)
+    np.testing.assert_allclose(o[0, 4:], 2.0)
+
+
+@pytest.mark.parametrize("Hq,Hkv,D", [(4, 2, 64), (32, 8, 128), (8, 8, 32)])
+def test_against_torch_sdpa_float64(Hq, Hkv, D):
+    rng = np.random.default_rng(Hq * 1000 + D)
+    B = 16
+    lens = [1, 15, 16, 17, 40, 100]
+    q, kp, vp, tables = _random_paged(rng, len(lens), Hq, Hkv, D, B, lens, 64)
+    o = paged_decode_f64(q, kp, vp, tables, lens, B)
+    G = Hq // Hkv
+    for i, n in enumerate(lens):
+        pk, pv, _, _ = gather_packed_kv(kp, vp, [tables[i]], [n], B)
+        kt = torch.from_numpy(np.repeat(pk, G, axis=1)).permute(1, 0, 2).unsqueeze(0)
+        vt = torch.from_numpy(np.repeat(pv, G, axis=1)).permute(1, 0, 2).unsqueeze(0)
+        qt = torch.from_numpy(q[i]).unsqueeze(0).unsqueeze(2)
+        ref = F.scaled_dot_product_attention(qt, kt, vt).squeeze(0).squeeze(1).numpy()
+        np.testing.assert_allclose(o[i], ref, rtol=1e-10, atol=1e-12)
+
+
+def test_reference_cpu_path_matches_f64():
+    rng = np.random.default_rng(7)
+    B, Hq, Hkv, D = 16, 8, 2, 64
+    lens = [3, 33, 70]
+    q, kp, vp, tables = _random_paged(rng, len(lens), Hq, Hkv, D, B, lens, 32)
+    o64 = paged_decode_f64(q, kp, vp, tables, lens, B)
+    o32 = reference_cpu_decode(
+        torch.from_numpy(q).float(), torch.from_numpy(kp).float(), torch.from_numpy(vp).float(),
+        tables, lens, B,
+    ).numpy()
+    np.testing.assert_allclose(o32, o64, rtol=1e-4, atol=1e-5)
