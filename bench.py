@@ -96,18 +96,19 @@ def main() -> int:
     import torch
 
     from mentat_amd import ops
+    from mentat_amd._lib import LAYOUT_NATIVE
     from mentat_amd.workloads import paged_decode_batch
 
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
     print("bench: building the workload", file=sys.stderr, flush=True)
-    b = paged_decode_batch(device=dev, seed=0)
+    b = paged_decode_batch(device=dev, seed=0, layout=LAYOUT_NATIVE)
     nbytes = b.algorithmic_bytes()
     out = torch.empty_like(b.q)
 
     def step():
-        ops.paged_decode(b.q, b.k_pool, b.v_pool, block_tables=b.block_tables, seq_lens=b.seq_lens,
-                         max_seqlen=b.max_seqlen, scale=b.scale, out=out)
+        ops.paged_decode(b.q, b.k_store, b.v_store, layout=b.layout, block_tables=b.block_tables,
+                         seq_lens=b.seq_lens, max_seqlen=b.max_seqlen, scale=b.scale, out=out)
 
     for _ in range(args.warmup):
         step()
@@ -159,6 +160,7 @@ def main() -> int:
             "context": "uniform [512, 4096], seed 0",
             "sum_context_tokens": sum(b.lens),
             "pool_pages": b.k_pool.shape[0],
+            "pool_layout": "native (K [page][kv head][slot][dim], V [page][kv head][dim][slot])",
             "algorithmic_bytes_per_step": nbytes,
         },
         "roofline": {

@@ -13,10 +13,11 @@
  * The library never allocates device memory: workspaces are passed in by the
  * caller, sized with the matching *_workspace_bytes() query.
  *
- * Pool layout (identical to the reference's PagedKVCacheManager pools,
- * core/paged_kv_cache.py:124-138): pool[num_blocks][block_size][num_kv_heads][head_dim],
- * row-major, in the model dtype. Block tables are int32, one row per sequence
- * slot, `table_stride` entries per row.
+ * Pools hold num_blocks pages of block_size tokens x num_kv_heads x head_dim
+ * elements in the model dtype, in one of two layouts (MENTAT_LAYOUT_* below);
+ * the reference layout is the reference's own PagedKVCacheManager pool
+ * (core/paged_kv_cache.py:124-138). Block tables are int32, one row per
+ * sequence slot, `table_stride` entries per row.
  *
  * dtype codes: MENTAT_F32 = 0, MENTAT_F16 = 1, MENTAT_BF16 = 2.
  */
@@ -39,6 +40,16 @@ extern "C" {
 #define MENTAT_F16 1
 #define MENTAT_BF16 2
 
+/* Pool layouts.
+ * MENTAT_LAYOUT_REFERENCE: K and V stored [num_blocks][block_size][Hkv][D]
+ *   (the reference's own layout).
+ * MENTAT_LAYOUT_NATIVE (16-bit dtypes, block_size a multiple of 16):
+ *   K stored [num_blocks][Hkv][block_size][D], V stored [num_blocks][Hkv][D][block_size],
+ *   so one (page, kv head) is contiguous and V is transposed inside it; this is
+ *   the layout the MFMA decode kernel reads. */
+#define MENTAT_LAYOUT_REFERENCE 0
+#define MENTAT_LAYOUT_NATIVE 1
+
 /* ABI version of this header; bumped on any signature change. */
 int mentat_abi_version(void);
 
@@ -57,6 +68,10 @@ int mentat_device_count(void);
  * tokens (the token appended this step included) with kv head
  * h / (Hq/Hkv) and softmax scale `scale`:  out[i,h] = softmax(q·Kᵀ·scale)·V.
  *
+ * `layout` selects the pool layout (MENTAT_LAYOUT_*). The native layout runs
+ * on the MFMA kernel with a persistent, equal-work (stream-K) partition of all
+ * (sequence, kv head, 16-token tile) triples; it needs block_tables.
+ *
  * Two addressing modes:
  *   paged  (block_tables != NULL): token t of sequence i lives in
  *          k_cache[block_tables[row*table_stride + t/block_size]][t%block_size],
@@ -72,10 +87,10 @@ int mentat_device_count(void);
  * Page ids outside [0, num_blocks) are skipped (treated as masked) rather
  * than read.
  * ---------------------------------------------------------------------- */
-size_t mentat_paged_decode_workspace_bytes(int N, int Hq, int Hkv, int D, int block_size,
+size_t mentat_paged_decode_workspace_bytes(int layout, int N, int Hq, int Hkv, int D, int block_size,
                                            int max_seqlen, int chunk_tokens);
 
-int mentat_paged_decode(const void* q, const void* k_cache, const void* v_cache,
+int mentat_paged_decode(int layout, const void* q, const void* k_cache, const void* v_cache,
                         const int32_t* block_tables, int64_t table_stride,
                         const int32_t* seq_rows, const int32_t* seq_lens,
                         const int32_t* cu_seqlens_k, int64_t num_blocks,
@@ -83,8 +98,50 @@ int mentat_paged_decode(const void* q, const void* k_cache, const void* v_cache,
                         int max_seqlen, float scale, int dtype, int chunk_tokens,
                         void* workspace, size_t workspace_bytes, void* stream);
 
-/* The chunk length (tokens) mentat_paged_decode uses when chunk_tokens == 0. */
+/* The chunk length (tokens) the reference-layout path uses when chunk_tokens == 0. */
 int mentat_paged_decode_auto_chunk(int N, int Hkv, int block_size, int max_seqlen);
+
+/* ------------------------------------------------------------------------
+ * KV append: write n new token rows into the pools, fused with the lazy
+ * copy-on-write of a shared tail page and the device block-table update.
+ *
+ * Replaces the device half of
+ *   core/paged_kv_cache.py:178-225  append_tokens (prefill: a while-loop over blocks)
+ *   core/paged_kv_cache.py:227-284  append_tokens_batched (decode: one token per sequence)
+ * The host keeps the reference's allocator/refcount bookkeeping and produces
+ * `plan`, int32 [7][n] (structure of arrays), one column per new token:
+ *   [0] dst block   [1] dst slot   [2] copy-on-write source block (-1: none)
+ *   [3] table row (-1: no table update)   [4] page index within the row
+ *   [5] new sequence length to store in seq_lens[row] (-1: leave)
+ *   [6] source token index into k_new / v_new
+ * A copy-on-write copies the source block's first `dst slot` tokens (the valid
+ * ones; the reference's copy_ also moves the unused tail slots, which no read
+ * ever reaches), so it never overlaps another write of the same launch.
+ * k_new/v_new: [n_src, Hkv, D] contiguous.
+ * block_tables ([table_rows, table_stride]) and seq_lens ([table_rows]) are the
+ * tables of this layer and may be NULL. Out-of-range plan entries are skipped.
+ * ---------------------------------------------------------------------- */
+int mentat_kv_append(int layout, const void* k_new, const void* v_new, void* k_pool, void* v_pool,
+                     const int32_t* plan, int n, int64_t n_src, int Hkv, int D, int block_size,
+                     int64_t num_blocks, int dtype, int32_t* block_tables, int64_t table_stride,
+                     int64_t table_rows, int32_t* seq_lens, void* stream);
+
+/* Batched whole-page copy dst[i] <- src[i] in each of n_pools pools (e.g. the
+ * K and V pools of every layer in one launch). `pools` is a DEVICE array of
+ * n_pools base pointers; block_bytes = bytes of one page. Pairs with an
+ * out-of-range id are skipped.
+ * Replaces the per-layer block copies of core/paged_kv_cache.py:201-206,
+ * :261-262 and :398-405 when many pages move at once. */
+int mentat_page_copy(void* const* pools, int n_pools, const int32_t* src, const int32_t* dst, int n,
+                     int64_t block_bytes, int64_t num_blocks, void* stream);
+
+/* Copy block-table rows (first n_entries entries) and lengths, for every layer:
+ * tables [L][rows][stride], seq_lens [L][rows] (may be NULL).
+ * The device half of fork_sequence, core/paged_kv_cache.py:152-170, whose
+ * host half copies the page-table lists and bumps the refcounts. */
+int mentat_table_copy_rows(int32_t* tables, int32_t* seq_lens, int L, int64_t rows, int64_t stride,
+                           const int32_t* src_rows, const int32_t* dst_rows, int n, int64_t n_entries,
+                           void* stream);
 
 #ifdef __cplusplus
 }

@@ -37,11 +37,12 @@ _c_u32 = ctypes.c_uint32
 SIGNATURES: dict[str, tuple] = {
     "mentat_abi_version": (_c_int, []),
     "mentat_device_count": (_c_int, []),
-    "mentat_paged_decode_workspace_bytes": (_c_size, [_c_int] * 7),
+    "mentat_paged_decode_workspace_bytes": (_c_size, [_c_int] * 8),
     "mentat_paged_decode_auto_chunk": (_c_int, [_c_int] * 4),
     "mentat_paged_decode": (
         _c_int,
         [
+            _c_int,  # layout
             _c_void_p, _c_void_p, _c_void_p,  # q, k_cache, v_cache
             _c_void_p, _c_i64,  # block_tables, table_stride
             _c_void_p, _c_void_p,  # seq_rows, seq_lens
@@ -51,7 +52,27 @@ SIGNATURES: dict[str, tuple] = {
             _c_void_p, _c_size, _c_void_p,  # workspace, workspace_bytes, stream
         ],
     ),
+    "mentat_kv_append": (
+        _c_int,
+        [
+            _c_int, _c_void_p, _c_void_p, _c_void_p, _c_void_p,  # layout, k_new, v_new, k_pool, v_pool
+            _c_void_p, _c_int, _c_i64, _c_int, _c_int, _c_int,  # plan, n, n_src, Hkv, D, block_size
+            _c_i64, _c_int, _c_void_p, _c_i64, _c_i64, _c_void_p,  # num_blocks, dtype, tables, stride, rows, lens
+            _c_void_p,  # stream
+        ],
+    ),
+    "mentat_page_copy": (
+        _c_int,
+        [_c_void_p, _c_int, _c_void_p, _c_void_p, _c_int, _c_i64, _c_i64, _c_void_p],
+    ),
+    "mentat_table_copy_rows": (
+        _c_int,
+        [_c_void_p, _c_void_p, _c_int, _c_i64, _c_i64, _c_void_p, _c_void_p, _c_int, _c_i64, _c_void_p],
+    ),
 }
+
+LAYOUT_REFERENCE = 0
+LAYOUT_NATIVE = 1
 
 
 class MentatError(RuntimeError):

@@ -21,10 +21,11 @@ enum PlanField { kDstBlock = 0, kDstSlot, kCowSrc, kRow, kPage, kNewLen, kSrcTok
 struct AppendParams {
   const char* k_new;  // [n_src, Hkv*D] elements
   const char* v_new;
-  char* k_pool;  // [num_blocks, B, Hkv*D]
+  char* k_pool;
   char* v_pool;
   const int32_t* plan;
   int n;
+  int Hkv, D, esz;
   long row_bytes;  // Hkv*D*esz: bytes of one cached token
   int block_size;
   long num_blocks;
@@ -33,8 +34,11 @@ struct AppendParams {
   long table_rows;
   int32_t* lens;  // this layer's [rows] (may be null)
   long n_src;
+  int layout;
 };
 
+// One workgroup per new token: optional whole-page copy-on-write, then the
+// token row, then the table entry and length.
 __global__ __launch_bounds__(256) void kv_append_kernel(AppendParams p) {
   const int i = blockIdx.x;
   if (i >= p.n) return;
@@ -47,30 +51,71 @@ __global__ __launch_bounds__(256) void kv_append_kernel(AppendParams p) {
   const int32_t src_tok = p.plan[kSrcTok * p.n + i];
   if (dst < 0 || dst >= p.num_blocks || slot < 0 || slot >= p.block_size) return;
   if (src_tok < 0 || src_tok >= p.n_src) return;
-  const long nvec = p.row_bytes / 16;  // 16-byte vectors per token row
   const long blk_bytes = (long)p.block_size * p.row_bytes;
 
-  // Lazy copy-on-write: the first `slot` (valid) tokens of the shared tail page.
-  if (cow >= 0 && cow < p.num_blocks && cow != dst) {
-    const long nv = (long)slot * nvec;
-    const uint4* sk = (const uint4*)(p.k_pool + (long)cow * blk_bytes);
-    const uint4* sv = (const uint4*)(p.v_pool + (long)cow * blk_bytes);
-    uint4* dk = (uint4*)(p.k_pool + (long)dst * blk_bytes);
-    uint4* dv = (uint4*)(p.v_pool + (long)dst * blk_bytes);
-    for (long j = threadIdx.x; j < nv; j += blockDim.x) {
-      dk[j] = sk[j];
-      dv[j] = sv[j];
+  // Copy-on-write of the shared tail page: its first `slot` (valid) tokens, K
+  // and V. Every other write of this launch targets slots >= slot of dst or a
+  // different block, so the copy needs no ordering against them.
+  if (cow >= 0 && cow < p.num_blocks && cow != dst && slot > 0) {
+    const char* ks = p.k_pool + (long)cow * blk_bytes;
+    const char* vs = p.v_pool + (long)cow * blk_bytes;
+    char* kd = p.k_pool + (long)dst * blk_bytes;
+    char* vd = p.v_pool + (long)dst * blk_bytes;
+    if (p.layout == MENTAT_LAYOUT_REFERENCE) {
+      const long nv = (long)slot * p.row_bytes / 16;
+      for (long j = threadIdx.x; j < nv; j += blockDim.x) {
+        ((uint4*)kd)[j] = ((const uint4*)ks)[j];
+        ((uint4*)vd)[j] = ((const uint4*)vs)[j];
+      }
+    } else {
+      // K [Hkv][B][D]: rows 0..slot-1 of each head are contiguous.
+      const long hv = (long)slot * p.D * p.esz / 16;  // vectors per head
+      const long hstride = (long)p.block_size * p.D * p.esz;
+      for (long j = threadIdx.x; j < (long)p.Hkv * hv; j += blockDim.x) {
+        const long h = j / hv, e = j - h * hv;
+        ((uint4*)(kd + h * hstride))[e] = ((const uint4*)(ks + h * hstride))[e];
+      }
+      // V [Hkv][D][B]: elements 0..slot-1 of every (head, d) row.
+      const long nel = (long)p.Hkv * p.D * slot;
+      for (long j = threadIdx.x; j < nel; j += blockDim.x) {
+        const long hd = j / slot, t = j - hd * slot;
+        const long idx = hd * p.block_size + t;
+        if (p.esz == 2) ((uint16_t*)vd)[idx] = ((const uint16_t*)vs)[idx];
+        else ((uint32_t*)vd)[idx] = ((const uint32_t*)vs)[idx];
+      }
     }
   }
-  // New token row.
-  {
-    const uint4* sk = (const uint4*)(p.k_new + (long)src_tok * p.row_bytes);
-    const uint4* sv = (const uint4*)(p.v_new + (long)src_tok * p.row_bytes);
-    uint4* dk = (uint4*)(p.k_pool + (long)dst * blk_bytes + (long)slot * p.row_bytes);
-    uint4* dv = (uint4*)(p.v_pool + (long)dst * blk_bytes + (long)slot * p.row_bytes);
+  const char* srck = p.k_new + (long)src_tok * p.row_bytes;
+  const char* srcv = p.v_new + (long)src_tok * p.row_bytes;
+  char* kblk = p.k_pool + (long)dst * blk_bytes;
+  char* vblk = p.v_pool + (long)dst * blk_bytes;
+  if (p.layout == MENTAT_LAYOUT_REFERENCE) {
+    // [B][Hkv][D]: the token row is contiguous.
+    const long nvec = p.row_bytes / 16;
+    const uint4* sk = (const uint4*)srck;
+    const uint4* sv = (const uint4*)srcv;
+    uint4* dk = (uint4*)(kblk + (long)slot * p.row_bytes);
+    uint4* dv = (uint4*)(vblk + (long)slot * p.row_bytes);
     for (long j = threadIdx.x; j < nvec; j += blockDim.x) {
       dk[j] = sk[j];
       dv[j] = sv[j];
+    }
+  } else {
+    // K: [Hkv][B][D] -> head h's D elements are contiguous at (h*B + slot)*D.
+    const long dvec = (long)p.D * p.esz / 16;
+    const long nvec = (long)p.Hkv * dvec;
+    for (long j = threadIdx.x; j < nvec; j += blockDim.x) {
+      const long h = j / dvec, e = j - h * dvec;
+      ((uint4*)(kblk + ((h * p.block_size + slot) * p.D) * p.esz))[e] = ((const uint4*)srck)[j];
+    }
+    // V: [Hkv][D][B] -> element (h, d) at ((h*D + d)*B + slot).
+    const long nel = (long)p.Hkv * p.D;
+    if (p.esz == 2) {
+      for (long j = threadIdx.x; j < nel; j += blockDim.x)
+        ((uint16_t*)vblk)[j * p.block_size + slot] = ((const uint16_t*)srcv)[j];
+    } else {
+      for (long j = threadIdx.x; j < nel; j += blockDim.x)
+        ((uint32_t*)vblk)[j * p.block_size + slot] = ((const uint32_t*)srcv)[j];
     }
   }
   if (threadIdx.x == 0 && row >= 0 && row < p.table_rows) {
@@ -141,8 +186,8 @@ static int esize(int dtype) {
   }
 }
 
-extern "C" int mentat_kv_append(const void* k_new, const void* v_new, void* k_pool, void* v_pool,
-                                const int32_t* plan, int n, int64_t n_src, int Hkv, int D,
+extern "C" int mentat_kv_append(int layout, const void* k_new, const void* v_new, void* k_pool,
+                                void* v_pool, const int32_t* plan, int n, int64_t n_src, int Hkv, int D,
                                 int block_size, int64_t num_blocks, int dtype, int32_t* block_tables,
                                 int64_t table_stride, int64_t table_rows, int32_t* seq_lens,
                                 void* stream) {
@@ -152,14 +197,16 @@ extern "C" int mentat_kv_append(const void* k_new, const void* v_new, void* k_po
   if (!k_new || !v_new || !k_pool || !v_pool || !plan || n < 0 || Hkv <= 0 || D <= 0 ||
       block_size <= 0 || num_blocks <= 0 || n_src <= 0)
     return MENTAT_EINVAL;
+  if (layout != MENTAT_LAYOUT_REFERENCE && layout != MENTAT_LAYOUT_NATIVE) return MENTAT_EINVAL;
   const long row_bytes = (long)Hkv * D * es;
-  if (row_bytes % 16 != 0) return MENTAT_EUNSUP;
+  if (((long)D * es) % 16 != 0) return MENTAT_EUNSUP;
   AppendParams p;
   p.k_new = (const char*)k_new; p.v_new = (const char*)v_new;
   p.k_pool = (char*)k_pool; p.v_pool = (char*)v_pool;
-  p.plan = plan; p.n = n; p.row_bytes = row_bytes; p.block_size = block_size; p.num_blocks = num_blocks;
+  p.plan = plan; p.n = n; p.Hkv = Hkv; p.D = D; p.esz = es;
+  p.row_bytes = row_bytes; p.block_size = block_size; p.num_blocks = num_blocks;
   p.tables = block_tables; p.table_stride = table_stride; p.table_rows = table_rows; p.lens = seq_lens;
-  p.n_src = n_src;
+  p.n_src = n_src; p.layout = layout;
   hipLaunchKernelGGL(kv_append_kernel, dim3(n), dim3(256), 0, (hipStream_t)stream, p);
   return (int)hipGetLastError();
 }

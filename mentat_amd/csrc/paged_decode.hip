@@ -287,16 +287,23 @@ extern "C" int mentat_paged_decode_auto_chunk(int N, int Hkv, int block_size, in
   return auto_chunk(N, Hkv, block_size, max_seqlen);
 }
 
-extern "C" size_t mentat_paged_decode_workspace_bytes(int N, int Hq, int Hkv, int D, int block_size,
-                                                      int max_seqlen, int chunk_tokens) {
-  if (N <= 0 || Hq <= 0 || D <= 0 || max_seqlen <= 0) return 0;
+size_t native_workspace_bytes(int N, int Hq, int Hkv, int D);
+int native_paged_decode(const void* q, const void* k_cache, const void* v_cache, const int32_t* block_tables,
+                        int64_t table_stride, const int32_t* seq_rows, const int32_t* seq_lens,
+                        int64_t num_blocks, void* out, int N, int Hq, int Hkv, int D, int block_size,
+                        float scale, int dtype, void* workspace, size_t workspace_bytes, hipStream_t stream);
+
+extern "C" size_t mentat_paged_decode_workspace_bytes(int layout, int N, int Hq, int Hkv, int D,
+                                                      int block_size, int max_seqlen, int chunk_tokens) {
+  if (N <= 0 || Hq <= 0 || Hkv <= 0 || D <= 0 || max_seqlen <= 0) return 0;
+  if (layout == MENTAT_LAYOUT_NATIVE) return native_workspace_bytes(N, Hq, Hkv, D);
   const int chunk = chunk_tokens > 0 ? chunk_tokens : auto_chunk(N, Hkv, block_size, max_seqlen);
   const int mc = ceil_div(max_seqlen, chunk);
   if (mc <= 1) return 0;
   return (size_t)N * Hq * mc * (D + 2) * sizeof(float);
 }
 
-extern "C" int mentat_paged_decode(const void* q, const void* k_cache, const void* v_cache,
+extern "C" int mentat_paged_decode(int layout, const void* q, const void* k_cache, const void* v_cache,
                                    const int32_t* block_tables, int64_t table_stride,
                                    const int32_t* seq_rows, const int32_t* seq_lens,
                                    const int32_t* cu_seqlens_k, int64_t num_blocks, void* out, int N,
@@ -310,6 +317,13 @@ extern "C" int mentat_paged_decode(const void* q, const void* k_cache, const voi
   if (paged && (!seq_lens || block_size <= 0 || table_stride <= 0 || num_blocks <= 0)) return MENTAT_EINVAL;
   if (!paged && !cu_seqlens_k) return MENTAT_EINVAL;
   if (max_seqlen < 0) return MENTAT_EINVAL;
+  if (layout == MENTAT_LAYOUT_NATIVE) {
+    if (!paged) return MENTAT_EINVAL;
+    return native_paged_decode(q, k_cache, v_cache, block_tables, table_stride, seq_rows, seq_lens, num_blocks,
+                               out, N, Hq, Hkv, D, block_size, scale, dtype, workspace, workspace_bytes,
+                               (hipStream_t)stream);
+  }
+  if (layout != MENTAT_LAYOUT_REFERENCE) return MENTAT_EINVAL;
   const int ms = max_seqlen > 0 ? max_seqlen : 1;
   DecodeParams p;
   p.q = q; p.k = k_cache; p.v = v_cache;

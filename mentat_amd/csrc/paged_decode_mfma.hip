@@ -1,0 +1,494 @@
+// Paged decode attention on the MFMA matrix cores (gfx950), native pool layout.
+//
+// Same semantics as paged_decode.hip (the gather + varlen attention of
+// core/paged_kv_cache.py:289-368 and adapters/attention_backend.py:192-229),
+// for 16-bit pools stored page-major and head-major:
+//     K store [num_blocks][Hkv][B][D]      (a page-head is B*D contiguous elements)
+//     V store [num_blocks][Hkv][D][B]      (transposed inside the page-head)
+// B must be a multiple of 16; a page is processed as B/16 tiles of 16 tokens.
+//
+// Per tile and kv head (one wavefront, all G = Hq/Hkv query heads of the group):
+//   S^T[16 tok x 16 q] = K[16 tok x D] . Q^T[D x 16 q]      v_mfma_f32_16x16x32_{bf16,f16}, D/32 steps
+//   O[16 q x 16 d]   += P[16 q x 16 tok] . V[16 tok x 16 d]  v_mfma_f32_16x16x16_{bf16,f16}, D/16 tiles
+// The accumulator layout of S^T (lane l: tokens 4*(l/16)+i, column q = l%16) is
+// exactly the A-operand layout of P for the second product, so the softmax
+// probabilities never leave their registers. Query rows q >= G are zero.
+// K rows load as 16 bytes per lane (16 tokens x 64 contiguous bytes per
+// instruction); V loads as 8 bytes per lane from the transposed page-head
+// (512 contiguous bytes per instruction).
+//
+// Online softmax in base 2, one (m, l) per column lane. The rescale of O is
+// lazy: the running max only moves when some column's tile max exceeds it by
+// more than 8 (probabilities stay <= 2^8 otherwise, exact in fp32/16-bit).
+//
+// Work partition (stream-K): all (sequence, kv head, tile) triples are laid
+// out in one flat index space; each of the W persistent wavefronts takes an
+// equal contiguous range. A wavefront whose range covers a whole (sequence,
+// kv head) unit writes the output directly; split units leave (m, l, O)
+// partials in the workspace at slot unit + wave, merged by combine_kernel.
+#include "mentat_common.h"
+
+namespace mentat {
+
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+template <typename T> struct Mfma;
+template <> struct Mfma<BF16> {
+  __device__ static f32x4_t qk(const uint4& a, const uint4& b, f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                   __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+  }
+  __device__ static f32x4_t pv(const uint2& a, const uint2& b, f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4_t, a),
+                                                     __builtin_bit_cast(s16x4_t, b), c, 0, 0, 0);
+  }
+  __device__ static uint2 pack(f32x4_t v) {
+    return __builtin_bit_cast(uint2, __builtin_convertvector(v, bf16x4_t));
+  }
+};
+template <> struct Mfma<F16> {
+  __device__ static f32x4_t qk(const uint4& a, const uint4& b, f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a),
+                                                  __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
+  }
+  __device__ static f32x4_t pv(const uint2& a, const uint2& b, f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4_t, a),
+                                                 __builtin_bit_cast(f16x4_t, b), c, 0, 0, 0);
+  }
+  __device__ static uint2 pack(f32x4_t v) {
+    return __builtin_bit_cast(uint2, __builtin_convertvector(v, f16x4_t));
+  }
+};
+
+struct NativeParams {
+  const void* q;
+  const void* k;
+  const void* v;
+  const int32_t* tables;
+  int64_t table_stride;
+  const int32_t* rows;
+  const int32_t* lens;
+  int64_t num_blocks;
+  void* out;
+  float* ws_o;       // [slots][G][D]
+  float* ws_ml;      // [slots][G][2]
+  int32_t* ws_meta;  // [0] tiles per wave, [1 .. N+1] tile prefix over sequences
+  int N, Hq, Hkv, B, W;
+  float scale_log2;
+};
+
+constexpr int kNativeMaxN = 4096;   // sequences per call (prefix table lives in LDS)
+constexpr int kNativeThreads = 256; // 4 wavefronts
+constexpr float kRescaleSlack = 8.f;
+
+__device__ __forceinline__ int seq_len_of(const NativeParams& p, int s) {
+  const int row = p.rows ? p.rows[s] : s;
+  const int n = p.lens[row];
+  return n > 0 ? n : 0;
+}
+
+// Block-wide tile prefix over the N sequences into s_prefix[0..N].
+__device__ void tile_prefix(const NativeParams& p, int32_t* s_prefix, int32_t* s_scan) {
+  const int tid = threadIdx.x;
+  const int per = (p.N + kNativeThreads - 1) / kNativeThreads;
+  const int base = tid * per;
+  int loc = 0;
+  for (int i = 0; i < per; ++i) {
+    const int s = base + i;
+    if (s < p.N) loc += (seq_len_of(p, s) + 15) >> 4;
+  }
+  s_scan[tid] = loc;
+  __syncthreads();
+  for (int off = 1; off < kNativeThreads; off <<= 1) {
+    const int v = tid >= off ? s_scan[tid - off] : 0;
+    __syncthreads();
+    s_scan[tid] += v;
+    __syncthreads();
+  }
+  int run = s_scan[tid] - loc;
+  for (int i = 0; i < per; ++i) {
+    const int s = base + i;
+    if (s < p.N) {
+      s_prefix[s] = run;
+      run += (seq_len_of(p, s) + 15) >> 4;
+    }
+  }
+  if (tid == kNativeThreads - 1) s_prefix[p.N] = s_scan[kNativeThreads - 1];
+  __syncthreads();
+}
+
+__device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
+
+// Wave-uniform reads through the constant address space compile to scalar
+// loads (s_load, counted by lgkmcnt), so they never wait behind the vector
+// loads of the K/V pipeline.
+typedef const int32_t __attribute__((address_space(4)))* const_i32_ptr;
+__device__ __forceinline__ int32_t scalar_load(const int32_t* p, long i) {
+  return ((const_i32_ptr)p)[i];
+}
+
+// Raw buffer resource over `bytes` bytes at `base` (gfx9 dword3). Loads at
+// offsets >= bytes return zero without touching memory, so a tile can always
+// be issued and is switched off by giving it a zero-sized resource.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes, 0x00020000);
+}
+
+template <typename T, int D, int G, int B>
+__global__ __launch_bounds__(kNativeThreads) void paged_decode_mfma_kernel(NativeParams p) {
+  static_assert(D % 32 == 0 && G >= 1 && G <= 16 && B % 16 == 0, "tile shape");
+  constexpr int KS = D / 32;  // QK k-steps
+  constexpr int NT = D / 16;  // PV column tiles
+  constexpr int NSUB = B / 16;  // tiles per page
+  using S = typename T::storage;
+
+  __shared__ int32_t s_prefix[kNativeMaxN + 1];
+  __shared__ int32_t s_scan[kNativeThreads];
+  tile_prefix(p, s_prefix, s_scan);
+
+  const int T_total = uniform(p.Hkv * s_prefix[p.N]);
+  const int tpw = (T_total + p.W - 1) / p.W;
+  if (blockIdx.x == 0) {
+    if (threadIdx.x == 0) p.ws_meta[0] = tpw;
+    for (int s = threadIdx.x; s <= p.N; s += kNativeThreads) p.ws_meta[1 + s] = s_prefix[s];
+  }
+  const int lane = threadIdx.x & 63;
+  const int wv = uniform(blockIdx.x * (kNativeThreads / 64) + (threadIdx.x >> 6));
+  int f = wv * tpw;
+  const int fend = min(T_total, f + tpw);
+  if (f >= fend) return;
+
+  // Unit containing f: last s with Hkv*prefix[s] <= f (upper_bound - 1).
+  int seq;
+  {
+    int lo = 0, hi = p.N;
+    while (lo < hi) {
+      const int mid = (lo + hi) >> 1;
+      if (p.Hkv * s_prefix[mid] <= f) lo = mid + 1; else hi = mid;
+    }
+    seq = uniform(lo - 1);
+  }
+  int pre = uniform(s_prefix[seq]);
+  int nt = uniform(s_prefix[seq + 1]) - pre;
+  int head = (f - p.Hkv * pre) / nt;
+  int tile = (f - p.Hkv * pre) - head * nt;
+
+  const int lr = lane & 15;  // tile row (K operand) / column (S^T, Q^T, O)
+  const int lg = lane >> 4;  // 4-lane-group index
+  // Lane-constant parts of the K and V addresses inside one 16-token tile.
+  const int k_lane = lr * D + 8 * lg;      // K [B][D] page-head: row lr, dims 8*lg..
+  const int v_lane = lr * B + 4 * lg;      // V [D][B] page-head: dim lr, tokens 4*lg..
+
+  while (f < fend) {
+    const int ustart = p.Hkv * pre + head * nt;
+    const int uend = ustart + nt;
+    const int seg_end = min(fend, uend);
+    const int t_first = tile;
+    const int t_last = tile + (seg_end - f);
+    const int row = p.rows ? scalar_load(p.rows, seq) : seq;
+    const int len = max(scalar_load(p.lens, row), 0);
+    const int32_t* trow = p.tables + (long)row * p.table_stride;
+
+    // Q^T operand: column q = lr holds Q[seq, head*G + q, 32s + 8*lg .. +8].
+    uint4 qo[KS];
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      if (lr < G) {
+        const S* qp = (const S*)p.q + ((long)seq * p.Hq + (long)head * G + lr) * D + 32 * s + 8 * lg;
+        qo[s] = *(const uint4*)qp;
+      } else {
+        qo[s] = make_uint4(0, 0, 0, 0);
+      }
+    }
+    float m = kNegInf, l = 0.f;
+    f32x4_t o[NT];
+#pragma unroll
+    for (int j = 0; j < NT; ++j) o[j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+    // Issue the loads of tile t. Tiles past the segment, and pages whose id is
+    // out of range, get a zero-sized resource: no memory traffic, zeros back.
+    auto load_tile = [&](int t, uint4 (&kr)[KS], uint2 (&vr)[NT], bool& okb) {
+      const int page = t / NSUB;
+      const int sub = t - page * NSUB;
+      int blk = -1;
+      if (t < t_last && page < p.table_stride) blk = scalar_load(trow, page);
+      okb = blk >= 0 && blk < p.num_blocks;
+      const long ph = ((okb ? (long)blk : 0L) * p.Hkv + head) * (long)(B * D);
+      const int bytes = okb ? B * D * (int)sizeof(S) : 0;
+      const __amdgpu_buffer_rsrc_t rk = make_rsrc((const S*)p.k + ph, bytes);
+      const __amdgpu_buffer_rsrc_t rv = make_rsrc((const S*)p.v + ph, bytes);
+      const int ksub = sub * 16 * D * (int)sizeof(S);
+      const int vsub = sub * 16 * (int)sizeof(S);
+#pragma unroll
+      for (int s = 0; s < KS; ++s)
+        kr[s] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
+                                              rk, (k_lane + 32 * s) * (int)sizeof(S), ksub, 0));
+#pragma unroll
+      for (int j = 0; j < NT; ++j)
+        vr[j] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(
+                                              rv, (v_lane + 16 * j * B) * (int)sizeof(S), vsub, 0));
+    };
+    auto compute_tile = [&](int t, bool okb, const uint4 (&kr)[KS], const uint2 (&vr)[NT]) {
+      f32x4_t st = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < KS; ++s) st = Mfma<T>::qk(kr[s], qo[s], st);
+      const int tok0 = t * 16 + 4 * lg;
+      float sc[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        sc[i] = st[i] * p.scale_log2;
+        if (!okb || tok0 + i >= len) sc[i] = kNegInf;
+      }
+      float pm = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
+      pm = fmaxf(pm, __shfl_xor(pm, 16));
+      pm = fmaxf(pm, __shfl_xor(pm, 32));
+      const bool grow = (m == kNegInf) ? (pm != kNegInf) : (pm > m + kRescaleSlack);
+      if (__builtin_amdgcn_ballot_w64(grow)) {
+        const float mn = fmaxf(m, pm);
+        const float alpha = (mn == kNegInf) ? 1.f : fast_exp2(m - mn);
+        l *= alpha;
+        m = mn;
+        // O rows are query heads 4*lg + i; their alpha sits in lane (4*lg + i).
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float ar = __shfl(alpha, 4 * lg + i);
+#pragma unroll
+          for (int j = 0; j < NT; ++j) o[j][i] *= ar;
+        }
+      }
+      const float ms = (m == kNegInf) ? 0.f : m;
+      f32x4_t pr;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) pr[i] = fast_exp2(sc[i] - ms);
+      float ps = (pr[0] + pr[1]) + (pr[2] + pr[3]);
+      ps += __shfl_xor(ps, 16);
+      ps += __shfl_xor(ps, 32);
+      l += ps;
+      const uint2 pa = Mfma<T>::pack(pr);
+#pragma unroll
+      for (int j = 0; j < NT; ++j) o[j] = Mfma<T>::pv(pa, vr[j], o[j]);
+    };
+
+    // Three-tile ring: tiles t+1 and t+2 are in flight while t is computed.
+    // Every load is issued unconditionally (past-the-end tiles are switched off
+    // through their resource), so the wait counts are exact on every path.
+    uint4 k0[KS], k1[KS], k2[KS];
+    uint2 v0[NT], v1[NT], v2[NT];
+    bool ok0, ok1, ok2;
+    load_tile(t_first, k0, v0, ok0);
+    load_tile(t_first + 1, k1, v1, ok1);
+    for (int t = t_first; t < t_last; t += 3) {
+      load_tile(t + 2, k2, v2, ok2);
+      compute_tile(t, ok0, k0, v0);
+      if (t + 1 >= t_last) break;
+      load_tile(t + 3, k0, v0, ok0);
+      compute_tile(t + 1, ok1, k1, v1);
+      if (t + 2 >= t_last) break;
+      load_tile(t + 4, k1, v1, ok1);
+      compute_tile(t + 2, ok2, k2, v2);
+    }
+
+    // Emit: O rows (query heads) 4*lg + i, columns d = 16 j + lr.
+    const bool whole = (f == ustart) && (seg_end == uend);
+    const long unit = (long)seq * p.Hkv + head;
+    if (whole) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int qrow = 4 * lg + i;
+        const float lq = __shfl(l, qrow);
+        if (qrow < G) {
+          const float inv = lq > 0.f ? 1.f / lq : 0.f;
+          const long ob = ((long)seq * p.Hq + (long)head * G + qrow) * D + lr;
+#pragma unroll
+          for (int j = 0; j < NT; ++j) Elem<T>::store1(p.out, ob + 16 * j, o[j][i] * inv);
+        }
+      }
+    } else {
+      const long slot = unit + wv;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int qrow = 4 * lg + i;
+        if (qrow < G) {
+          float* wo = p.ws_o + (slot * G + qrow) * D + lr;
+#pragma unroll
+          for (int j = 0; j < NT; ++j) wo[16 * j] = o[j][i];
+        }
+      }
+      if (lane < G) {
+        p.ws_ml[(slot * G + lane) * 2] = m;
+        p.ws_ml[(slot * G + lane) * 2 + 1] = l;
+      }
+    }
+
+    f = seg_end;
+    if (f >= fend) break;
+    // Next unit (skip sequences without tokens).
+    ++head;
+    tile = 0;
+    if (head == p.Hkv) {
+      head = 0;
+      ++seq;
+      while (seq < p.N && s_prefix[seq + 1] == s_prefix[seq]) ++seq;
+      if (seq >= p.N) break;
+      seq = uniform(seq);
+      pre = uniform(s_prefix[seq]);
+      nt = uniform(s_prefix[seq + 1]) - pre;
+    }
+  }
+}
+
+// Merge split units; write zeros for sequences without cached tokens.
+// grid: N * Hkv workgroups (one per unit) of one wavefront; lane l owns the
+// E = G*D/64 consecutive outputs starting at l*E of the unit's [G][D] block.
+// Pieces are merged online (running max, sum and rescaled accumulator).
+template <typename T, int D, int G>
+__global__ __launch_bounds__(64) void native_combine_kernel(NativeParams p) {
+  constexpr int E = G * D / 64;
+  static_assert(E >= 1 && (E % 2 == 0 || E == 1), "combine lane split");
+  const long unit = blockIdx.x;
+  const int head = (int)(unit % p.Hkv);
+  const int seq = (int)(unit / p.Hkv);
+  if (seq >= p.N) return;
+  const int lane = threadIdx.x;
+  const int g = (lane * E) / D;
+  const int d0 = (lane * E) - g * D;
+  const long ob = ((long)seq * p.Hq + (long)head * G + g) * D + d0;
+  const int pre = scalar_load(p.ws_meta + 1, seq);
+  const int nt = scalar_load(p.ws_meta + 1, seq + 1) - pre;
+  const int tpw = scalar_load(p.ws_meta, 0);
+  if (nt == 0) {
+#pragma unroll
+    for (int e = 0; e < E; ++e) Elem<T>::store1(p.out, ob + e, 0.f);
+    return;
+  }
+  const int ustart = p.Hkv * pre + head * nt;
+  const int w0 = ustart / tpw;
+  const int w1 = (ustart + nt - 1) / tpw;
+  if (w0 == w1) return;  // written by the main kernel
+  float M = kNegInf, L = 0.f, acc[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) acc[e] = 0.f;
+  for (int w = w0; w <= w1; ++w) {
+    const long slot = unit + w;
+    const float mp = p.ws_ml[(slot * G + g) * 2];
+    const float lp = p.ws_ml[(slot * G + g) * 2 + 1];
+    float op[E];
+    const float* wo = p.ws_o + (slot * G + g) * D + d0;
+#pragma unroll
+    for (int e = 0; e < E; ++e) op[e] = wo[e];
+    const float mn = fmaxf(M, mp);
+    const float ms = (mn == kNegInf) ? 0.f : mn;
+    const float a = fast_exp2(M - ms), b = fast_exp2(mp - ms);
+    L = L * a + lp * b;
+#pragma unroll
+    for (int e = 0; e < E; ++e) acc[e] = acc[e] * a + op[e] * b;
+    M = mn;
+  }
+  const float inv = L > 0.f ? 1.f / L : 0.f;
+#pragma unroll
+  for (int e = 0; e < E; ++e) Elem<T>::store1(p.out, ob + e, acc[e] * inv);
+}
+
+template <typename T, int D, int G, int B>
+static int launch_native(const NativeParams& p, hipStream_t stream) {
+  hipLaunchKernelGGL((paged_decode_mfma_kernel<T, D, G, B>), dim3(p.W / 4), dim3(kNativeThreads), 0, stream, p);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return (int)e;
+  hipLaunchKernelGGL((native_combine_kernel<T, D, G>), dim3((unsigned)((long)p.N * p.Hkv)), dim3(64), 0,
+                     stream, p);
+  return (int)hipGetLastError();
+}
+
+template <typename T, int D, int G>
+static int native_b(const NativeParams& p, hipStream_t s) {
+  switch (p.B) {
+    case 16: return launch_native<T, D, G, 16>(p, s);
+    case 32: return launch_native<T, D, G, 32>(p, s);
+    case 64: return launch_native<T, D, G, 64>(p, s);
+    default: return MENTAT_EUNSUP;
+  }
+}
+
+template <typename T, int D>
+static int native_g(int G, const NativeParams& p, hipStream_t s) {
+  switch (G) {
+    case 1: return native_b<T, D, 1>(p, s);
+    case 2: return native_b<T, D, 2>(p, s);
+    case 4: return native_b<T, D, 4>(p, s);
+    case 8: return native_b<T, D, 8>(p, s);
+    case 16: return native_b<T, D, 16>(p, s);
+    default: return MENTAT_EUNSUP;
+  }
+}
+
+template <typename T>
+static int native_d(int D, int G, const NativeParams& p, hipStream_t s) {
+  switch (D) {
+    case 64: return native_g<T, 64>(G, p, s);
+    case 128: return native_g<T, 128>(G, p, s);
+    default: return MENTAT_EUNSUP;
+  }
+}
+
+// Persistent grid size: resident wavefronts of the current device, rounded to
+// whole workgroups. Cached per device.
+static int persistent_waves() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+  if (cached[dev] > 0) return cached[dev];
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+    cus = 256;
+  int blocks = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, paged_decode_mfma_kernel<BF16, 128, 4, 16>,
+                                                   kNativeThreads, 0) != hipSuccess || blocks <= 0)
+    blocks = 2;
+  cached[dev] = cus * blocks * (kNativeThreads / 64);
+  return cached[dev];
+}
+
+}  // namespace mentat
+
+using namespace mentat;
+
+// Workspace of the native path: partial slots (units + waves), metadata.
+size_t native_workspace_bytes(int N, int Hq, int Hkv, int D) {
+  const int W = persistent_waves();
+  const int G = Hq / Hkv;
+  const size_t slots = (size_t)N * Hkv + W;
+  const size_t fl = slots * G * (D + 2);
+  return fl * sizeof(float) + (size_t)(N + 2) * sizeof(int32_t) + 256;
+}
+
+int native_paged_decode(const void* q, const void* k_cache, const void* v_cache, const int32_t* block_tables,
+                        int64_t table_stride, const int32_t* seq_rows, const int32_t* seq_lens,
+                        int64_t num_blocks, void* out, int N, int Hq, int Hkv, int D, int block_size,
+                        float scale, int dtype, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  if (N > kNativeMaxN) return MENTAT_EUNSUP;
+  if (block_size != 16 && block_size != 32 && block_size != 64) return MENTAT_EUNSUP;
+  if (!block_tables || !seq_lens || table_stride <= 0 || num_blocks <= 0) return MENTAT_EINVAL;
+  const size_t need = native_workspace_bytes(N, Hq, Hkv, D);
+  if (!workspace || workspace_bytes < need) return MENTAT_ESPACE;
+  NativeParams p;
+  p.q = q; p.k = k_cache; p.v = v_cache;
+  p.tables = block_tables; p.table_stride = table_stride; p.rows = seq_rows; p.lens = seq_lens;
+  p.num_blocks = num_blocks; p.out = out;
+  p.N = N; p.Hq = Hq; p.Hkv = Hkv; p.B = block_size; p.W = persistent_waves();
+  p.scale_log2 = scale * kLog2e;
+  const int G = Hq / Hkv;
+  const size_t slots = (size_t)N * Hkv + p.W;
+  p.ws_o = (float*)workspace;
+  p.ws_ml = p.ws_o + slots * G * D;
+  p.ws_meta = (int32_t*)(p.ws_ml + slots * G * 2);
+  switch (dtype) {
+    case MENTAT_BF16: return native_d<BF16>(D, G, p, stream);
+    case MENTAT_F16: return native_d<F16>(D, G, p, stream);
+    default: return MENTAT_EUNSUP;
+  }
+}

@@ -11,9 +11,31 @@ from typing import Optional
 
 import torch
 
-from ._lib import DTYPE_CODES, MentatError, check, get_lib, ptr, stream_handle
+from ._lib import (
+    DTYPE_CODES,
+    LAYOUT_NATIVE,
+    LAYOUT_REFERENCE,
+    MentatError,
+    check,
+    get_lib,
+    ptr,
+    stream_handle,
+)
 
-__all__ = ["paged_decode", "MentatError", "workspace"]
+__all__ = [
+    "paged_decode",
+    "kv_append",
+    "page_copy",
+    "table_copy_rows",
+    "MentatError",
+    "workspace",
+    "LAYOUT_NATIVE",
+    "LAYOUT_REFERENCE",
+    "PLAN_FIELDS",
+]
+
+# Rows of the int32 [7, n] append plan (see mentat_kv_append in include/mentat_capi.h).
+PLAN_FIELDS = ("dst_block", "dst_slot", "cow_src", "row", "page", "new_len", "src_tok")
 
 # One workspace per (device, stream): calls on one stream are ordered, so they
 # may share it; calls on different streams get different buffers.
@@ -59,11 +81,15 @@ def paged_decode(
     scale: Optional[float] = None,
     chunk_tokens: int = 0,
     out: Optional[torch.Tensor] = None,
+    layout: int = LAYOUT_REFERENCE,
 ) -> torch.Tensor:
     """One-query-per-sequence attention over a paged (or packed varlen) KV cache.
 
     Paged mode (``block_tables`` given): k_cache/v_cache are pools
-    ``[num_blocks, block_size, Hkv, D]``; sequence i uses table row
+    ``[num_blocks, block_size, Hkv, D]`` (``layout=LAYOUT_REFERENCE``), or the
+    native stores K ``[num_blocks, Hkv, block_size, D]`` and V
+    ``[num_blocks, Hkv, D, block_size]`` (``layout=LAYOUT_NATIVE``, 16-bit
+    dtypes, block_size a multiple of 16); sequence i uses table row
     ``seq_rows[i]`` (or i) and has ``seq_lens[row]`` tokens.
     Packed mode: k_cache/v_cache are ``[total, Hkv, D]`` and ``cu_seqlens_k``
     (int32, N+1) delimits the sequences, as in the reference's
@@ -81,12 +107,23 @@ def paged_decode(
     _require(k_cache.device == dev and v_cache.device == dev, "q/k/v devices differ")
     _require(q.is_contiguous() and k_cache.is_contiguous() and v_cache.is_contiguous(),
              "q, k_cache and v_cache must be contiguous")
-    _require(k_cache.shape == v_cache.shape, "k_cache and v_cache shapes differ")
     if scale is None:
         scale = 1.0 / math.sqrt(D)
+    if layout == LAYOUT_NATIVE:
+        _require(block_tables is not None, "the native layout needs block_tables")
+        _require(q.dtype in (torch.bfloat16, torch.float16), "the native layout needs a 16-bit dtype")
+        _require(k_cache.dim() == 4 and v_cache.dim() == 4, "native stores are 4-d")
+        num_blocks, Hkv, block_size, Dk = k_cache.shape
+        _require(tuple(v_cache.shape) == (num_blocks, Hkv, Dk, block_size),
+                 "native V store must be [num_blocks, Hkv, D, block_size]")
+        _require(block_size % 16 == 0, "the native layout needs block_size % 16 == 0")
+    else:
+        _require(layout == LAYOUT_REFERENCE, f"unknown layout {layout}")
+        _require(k_cache.shape == v_cache.shape, "k_cache and v_cache shapes differ")
     if block_tables is not None:
-        _require(k_cache.dim() == 4, "paged k_cache must be [num_blocks, block_size, Hkv, D]")
-        num_blocks, block_size, Hkv, Dk = k_cache.shape
+        if layout == LAYOUT_REFERENCE:
+            _require(k_cache.dim() == 4, "paged k_cache must be [num_blocks, block_size, Hkv, D]")
+            num_blocks, block_size, Hkv, Dk = k_cache.shape
         _require(seq_lens is not None, "paged mode needs seq_lens")
         _require(block_tables.dim() == 2, "block_tables must be [rows, stride]")
         _check_i32(block_tables, "block_tables", dev)
@@ -118,10 +155,11 @@ def paged_decode(
         return out
     lib = get_lib()
     max_seqlen = max(int(max_seqlen), 1)
-    nbytes = lib.mentat_paged_decode_workspace_bytes(N, Hq, Hkv, D, block_size, max_seqlen, chunk_tokens)
+    nbytes = lib.mentat_paged_decode_workspace_bytes(layout, N, Hq, Hkv, D, block_size, max_seqlen,
+                                                     chunk_tokens)
     ws = workspace(dev, nbytes) if nbytes else None
     st = lib.mentat_paged_decode(
-        ptr(q), ptr(k_cache), ptr(v_cache),
+        layout, ptr(q), ptr(k_cache), ptr(v_cache),
         ptr(block_tables), stride,
         ptr(seq_rows), ptr(seq_lens),
         ptr(cu_seqlens_k), num_blocks,
@@ -131,3 +169,98 @@ def paged_decode(
     )
     check(st, "mentat_paged_decode")
     return out
+
+
+def kv_append(
+    k_new: torch.Tensor,
+    v_new: torch.Tensor,
+    k_store: torch.Tensor,
+    v_store: torch.Tensor,
+    plan: torch.Tensor,
+    *,
+    block_size: int,
+    layout: int = LAYOUT_REFERENCE,
+    block_tables: Optional[torch.Tensor] = None,
+    seq_lens: Optional[torch.Tensor] = None,
+) -> None:
+    """Write new token rows into the pools per ``plan`` (int32 [7, n], PLAN_FIELDS).
+
+    Fused with the lazy copy-on-write of shared tail pages and the device
+    table/length update of this layer (``block_tables`` [rows, stride],
+    ``seq_lens`` [rows]). k_new/v_new: [n_src, Hkv, D].
+    """
+    dev = k_store.device
+    _require(dev.type == "cuda", "kv_append runs on the GPU only")
+    _require(plan.dim() == 2 and plan.shape[0] == len(PLAN_FIELDS), "plan must be int32 [7, n]")
+    _check_i32(plan, "plan", dev)
+    _check_i32(block_tables, "block_tables", dev)
+    _check_i32(seq_lens, "seq_lens", dev)
+    _require(k_new.dim() == 3 and k_new.shape == v_new.shape, "k_new/v_new must be [n, Hkv, D]")
+    _require(k_new.is_contiguous() and v_new.is_contiguous(), "k_new/v_new must be contiguous")
+    _require(k_new.dtype == k_store.dtype == v_store.dtype == v_new.dtype, "dtype mismatch")
+    _require(k_store.is_contiguous() and v_store.is_contiguous(), "stores must be contiguous")
+    n_src, Hkv, D = k_new.shape
+    num_blocks = k_store.shape[0]
+    if layout == LAYOUT_NATIVE:
+        _require(tuple(k_store.shape) == (num_blocks, Hkv, block_size, D), "bad native K store")
+        _require(tuple(v_store.shape) == (num_blocks, Hkv, D, block_size), "bad native V store")
+    else:
+        _require(tuple(k_store.shape) == (num_blocks, block_size, Hkv, D), "bad K pool")
+        _require(tuple(v_store.shape) == (num_blocks, block_size, Hkv, D), "bad V pool")
+    n = plan.shape[1]
+    if n == 0:
+        return
+    rows = stride = 0
+    if block_tables is not None:
+        _require(block_tables.dim() == 2, "block_tables must be [rows, stride]")
+        rows, stride = block_tables.shape
+        _require(block_tables.stride(0) == stride, "block_tables rows must be dense")
+        if seq_lens is not None:
+            _require(seq_lens.numel() >= rows, "seq_lens shorter than block_tables")
+    elif seq_lens is not None:
+        rows = seq_lens.numel()
+    st = get_lib().mentat_kv_append(
+        layout, ptr(k_new), ptr(v_new), ptr(k_store), ptr(v_store), ptr(plan), n, n_src, Hkv, D,
+        block_size, num_blocks, DTYPE_CODES[k_store.dtype], ptr(block_tables), stride, rows,
+        ptr(seq_lens), stream_handle(dev),
+    )
+    check(st, "mentat_kv_append")
+
+
+def page_copy(pools: list, src: torch.Tensor, dst: torch.Tensor) -> None:
+    """dst[i] <- src[i] (whole pages) in every pool of ``pools`` with one launch."""
+    if not pools or src.numel() == 0:
+        return
+    dev = pools[0].device
+    _check_i32(src, "src", dev)
+    _check_i32(dst, "dst", dev)
+    _require(src.numel() == dst.numel(), "src/dst lengths differ")
+    nb = pools[0].shape[0]
+    bb = pools[0][0].numel() * pools[0].element_size()
+    for t in pools:
+        _require(t.is_contiguous() and t.device == dev, "pools must be contiguous on one device")
+        _require(t.shape[0] == nb and t[0].numel() * t.element_size() == bb, "pools differ in geometry")
+    ptrs = torch.tensor([t.data_ptr() for t in pools], dtype=torch.int64, device=dev)
+    st = get_lib().mentat_page_copy(ptr(ptrs), len(pools), ptr(src), ptr(dst), src.numel(), bb, nb,
+                                    stream_handle(dev))
+    check(st, "mentat_page_copy")
+
+
+def table_copy_rows(tables: torch.Tensor, seq_lens: Optional[torch.Tensor], src_rows: torch.Tensor,
+                    dst_rows: torch.Tensor, n_entries: int) -> None:
+    """tables[:, dst] <- tables[:, src] (first n_entries entries) and lengths, all layers."""
+    if src_rows.numel() == 0:
+        return
+    dev = tables.device
+    _check_i32(tables, "tables", dev)
+    _check_i32(seq_lens, "seq_lens", dev)
+    _check_i32(src_rows, "src_rows", dev)
+    _check_i32(dst_rows, "dst_rows", dev)
+    _require(tables.dim() == 3, "tables must be [L, rows, stride]")
+    L, rows, stride = tables.shape
+    if seq_lens is not None:
+        _require(tuple(seq_lens.shape) == (L, rows), "seq_lens must be [L, rows]")
+    _require(0 <= n_entries <= stride, "n_entries out of range")
+    st = get_lib().mentat_table_copy_rows(ptr(tables), ptr(seq_lens), L, rows, stride, ptr(src_rows),
+                                          ptr(dst_rows), src_rows.numel(), n_entries, stream_handle(dev))
+    check(st, "mentat_table_copy_rows")

@@ -2,7 +2,8 @@
 
 These are the measured workloads (sizes, distributions and seeds fixed here):
 
-* ``paged_decode_batch``: paged decode at Llama-3-8B attention shapes —
+* ``paged_decode_batch``: paged decode at Llama-3-8B attention shapes (pools
+  in either layout) —
   bf16, 32 query / 8 kv heads, head_dim 128, page size 16, 64 sequences with
   context lengths uniform in [512, 4096], block tables = consecutive slices of
   a seeded random permutation of a 65,536-page pool, Q/K/V ~ N(0, 1),
@@ -16,17 +17,37 @@ import numpy as np
 import torch
 
 
+from ._lib import LAYOUT_NATIVE, LAYOUT_REFERENCE
+
+
+def logical_views(k_store: torch.Tensor, v_store: torch.Tensor, layout: int):
+    """[num_blocks, B, Hkv, D]-shaped views of K/V stores of either layout."""
+    if layout == LAYOUT_NATIVE:
+        return k_store.permute(0, 2, 1, 3), v_store.permute(0, 3, 1, 2)
+    return k_store, v_store
+
+
 @dataclass
 class PagedBatch:
     q: torch.Tensor            # [N, Hq, D]
-    k_pool: torch.Tensor       # [num_blocks, B, Hkv, D]
-    v_pool: torch.Tensor
+    k_store: torch.Tensor      # pool storage in `layout`
+    v_store: torch.Tensor
     block_tables: torch.Tensor  # [N, max_pages] int32 (unused entries = 0)
     seq_lens: torch.Tensor     # [N] int32
     lens: list                 # host copy of seq_lens
     tables: list               # host page tables (list of lists)
     block_size: int
     scale: float
+    layout: int = LAYOUT_REFERENCE
+
+    @property
+    def k_pool(self) -> torch.Tensor:
+        """K as [num_blocks, B, Hkv, D] (a view; non-contiguous for the native layout)."""
+        return logical_views(self.k_store, self.v_store, self.layout)[0]
+
+    @property
+    def v_pool(self) -> torch.Tensor:
+        return logical_views(self.k_store, self.v_store, self.layout)[1]
 
     @property
     def max_seqlen(self) -> int:
@@ -39,7 +60,7 @@ class PagedBatch:
         written once, one int32 table entry per page and one length per sequence.
         """
         N, Hq, D = self.q.shape
-        Hkv = self.k_pool.shape[2]
+        Hkv = self.k_pool.shape[2]  # logical [num_blocks, B, Hkv, D]
         esz = self.q.element_size()
         ctx = sum(self.lens)
         pages = sum((n + self.block_size - 1) // self.block_size for n in self.lens)
@@ -60,6 +81,7 @@ def paged_decode_batch(
     device: str | torch.device = "cuda",
     seed: int = 0,
     lens: list | None = None,
+    layout: int = LAYOUT_REFERENCE,
 ) -> PagedBatch:
     rng = np.random.default_rng(seed)
     if lens is None:
@@ -83,18 +105,24 @@ def paged_decode_batch(
     g = torch.Generator(device=device)
     g.manual_seed(seed)
     q = torch.randn(N, Hq, D, generator=g, device=device, dtype=torch.float32).to(dtype)
-    k_pool = torch.empty(num_blocks, block_size, Hkv, D, device=device, dtype=dtype)
-    v_pool = torch.empty_like(k_pool)
-    # Fill in slices to bound the fp32 temporaries.
+    if layout == LAYOUT_NATIVE:
+        k_store = torch.empty(num_blocks, Hkv, block_size, D, device=device, dtype=dtype)
+        v_store = torch.empty(num_blocks, Hkv, D, block_size, device=device, dtype=dtype)
+    else:
+        k_store = torch.empty(num_blocks, block_size, Hkv, D, device=device, dtype=dtype)
+        v_store = torch.empty_like(k_store)
+    # Fill in slices to bound the fp32 temporaries (i.i.d. entries: the layout
+    # does not change the distribution).
     step = max(1, (1 << 26) // (block_size * Hkv * D))
     for s in range(0, num_blocks, step):
         e = min(num_blocks, s + step)
-        k_pool[s:e] = torch.randn(e - s, block_size, Hkv, D, generator=g, device=device).to(dtype)
-        v_pool[s:e] = torch.randn(e - s, block_size, Hkv, D, generator=g, device=device).to(dtype)
+        k_store[s:e] = torch.randn(k_store[s:e].shape, generator=g, device=device).to(dtype)
+        v_store[s:e] = torch.randn(v_store[s:e].shape, generator=g, device=device).to(dtype)
     return PagedBatch(
         q=q,
-        k_pool=k_pool,
-        v_pool=v_pool,
+        k_store=k_store,
+        v_store=v_store,
+        layout=layout,
         block_tables=torch.from_numpy(tab).to(device),
         seq_lens=torch.tensor(lens, dtype=torch.int32, device=device),
         lens=lens,

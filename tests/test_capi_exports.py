@@ -29,8 +29,8 @@ def test_abi_version_and_pure_host_queries():
     lib = _lib.get_lib()
     assert lib.mentat_abi_version() >= 1
     # Pure host arithmetic: no device needed.
-    assert lib.mentat_paged_decode_workspace_bytes(0, 32, 8, 128, 16, 4096, 0) == 0
-    nb = lib.mentat_paged_decode_workspace_bytes(64, 32, 8, 128, 16, 4096, 256)
+    assert lib.mentat_paged_decode_workspace_bytes(0, 0, 32, 8, 128, 16, 4096, 0) == 0
+    nb = lib.mentat_paged_decode_workspace_bytes(0, 64, 32, 8, 128, 16, 4096, 256)
     assert nb == 64 * 32 * 16 * (128 + 2) * 4
     c = lib.mentat_paged_decode_auto_chunk(64, 8, 16, 4096)
     assert c % 16 == 0 and 16 <= c <= 4096

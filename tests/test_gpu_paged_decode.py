@@ -9,6 +9,7 @@ import pytest
 import torch
 
 from mentat_amd import ops
+from mentat_amd._lib import LAYOUT_NATIVE, LAYOUT_REFERENCE
 from mentat_amd.workloads import paged_decode_batch
 from oracle.attention import paged_decode_f64, sdpa_decode_f64
 
@@ -43,15 +44,80 @@ CASES = [
 @pytest.mark.parametrize("Hq,Hkv,D,dtype,lens", CASES)
 @pytest.mark.parametrize("chunk", [0, 16, 64])
 def test_paged_matches_oracle(gpu, Hq, Hkv, D, dtype, lens, chunk):
-    print(f"case Hq={Hq} Hkv={Hkv} D={D} {dtype} lens={lens} chunk={chunk}", flush=True)
+    print(f"case reference layout Hq={Hq} Hkv={Hkv} D={D} {dtype} lens={lens} chunk={chunk}", flush=True)
     b = paged_decode_batch(N=len(lens), Hq=Hq, Hkv=Hkv, D=D, dtype=dtype, device=gpu,
                            num_blocks=256, lens=lens, seed=len(lens) + D)
-    out = ops.paged_decode(b.q, b.k_pool, b.v_pool, block_tables=b.block_tables,
+    out = ops.paged_decode(b.q, b.k_store, b.v_store, layout=b.layout, block_tables=b.block_tables,
                            seq_lens=b.seq_lens, max_seqlen=b.max_seqlen, chunk_tokens=chunk,
                            scale=b.scale)
     torch.cuda.synchronize()
     atol, rtol = TOL[dtype]
     np.testing.assert_allclose(_to64(out), _oracle(b), atol=atol, rtol=rtol)
+
+
+NATIVE_CASES = [
+    # (Hq, Hkv, D, dtype, block_size, lens)
+    (32, 8, 128, torch.bfloat16, 16, [1, 15, 16, 17, 250, 513]),
+    (16, 8, 128, torch.bfloat16, 16, [5, 77, 1000]),
+    (8, 8, 64, torch.float16, 16, [16, 48, 300]),
+    (16, 2, 128, torch.bfloat16, 32, [33, 700, 0, 64]),
+    (32, 2, 128, torch.bfloat16, 16, [2, 40]),
+    (4, 4, 64, torch.bfloat16, 64, [3, 90, 129]),
+    (64, 8, 128, torch.bfloat16, 16, [100]),
+]
+
+
+@pytest.mark.parametrize("Hq,Hkv,D,dtype,bs,lens", NATIVE_CASES)
+def test_native_layout_matches_oracle(gpu, Hq, Hkv, D, dtype, bs, lens):
+    print(f"case native layout Hq={Hq} Hkv={Hkv} D={D} {dtype} B={bs} lens={lens}", flush=True)
+    b = paged_decode_batch(N=len(lens), Hq=Hq, Hkv=Hkv, D=D, dtype=dtype, device=gpu, block_size=bs,
+                           num_blocks=256, lens=lens, seed=len(lens) + D + 7, layout=LAYOUT_NATIVE)
+    out = ops.paged_decode(b.q, b.k_store, b.v_store, layout=LAYOUT_NATIVE, block_tables=b.block_tables,
+                           seq_lens=b.seq_lens, max_seqlen=max(1, b.max_seqlen), scale=b.scale)
+    torch.cuda.synchronize()
+    atol, rtol = TOL[dtype]
+    np.testing.assert_allclose(_to64(out), _oracle(b), atol=atol, rtol=rtol)
+
+
+def test_native_many_sequences_stream_k(gpu):
+    # Many short and long sequences: units split across persistent wavefronts.
+    rng = np.random.default_rng(9)
+    lens = rng.integers(1, 700, size=300).tolist()
+    b = paged_decode_batch(N=len(lens), Hq=32, Hkv=8, D=128, device=gpu, num_blocks=16384,
+                           lens=lens, seed=9, layout=LAYOUT_NATIVE)
+    out = ops.paged_decode(b.q, b.k_store, b.v_store, layout=LAYOUT_NATIVE, block_tables=b.block_tables,
+                           seq_lens=b.seq_lens, max_seqlen=b.max_seqlen, scale=b.scale)
+    torch.cuda.synchronize()
+    o = _to64(out)
+    q64 = _to64(b.q)
+    for i in range(0, len(lens), 7):
+        pages = torch.tensor(b.tables[i], dtype=torch.long, device=gpu)
+        kp = _to64(b.k_pool[pages]).reshape(-1, 8, 128)[: lens[i]]
+        vp = _to64(b.v_pool[pages]).reshape(-1, 8, 128)[: lens[i]]
+        ref = sdpa_decode_f64(q64[i:i + 1], kp, vp, np.array([0, lens[i]]), b.scale)
+        np.testing.assert_allclose(o[i], ref[0], atol=2e-2, rtol=1e-2, err_msg=f"seq {i}")
+
+
+def test_native_seq_rows_and_bad_pages(gpu):
+    b = paged_decode_batch(N=4, Hq=32, Hkv=8, D=128, device=gpu, num_blocks=64, lens=[40, 3, 200, 16],
+                           seed=4, layout=LAYOUT_NATIVE)
+    rows = [2, 0, 2, 3, 1]
+    rows_t = torch.tensor(rows, dtype=torch.int32, device=gpu)
+    g = torch.Generator(device=gpu).manual_seed(1)
+    q = torch.randn(5, 32, 128, device=gpu, generator=g).to(torch.bfloat16)
+    bad = b.block_tables.clone()
+    bad[1, 0] = -5  # row 1 (3 tokens) loses its only page -> zero output
+    out = ops.paged_decode(q, b.k_store, b.v_store, layout=LAYOUT_NATIVE, block_tables=bad,
+                           seq_lens=b.seq_lens, seq_rows=rows_t, max_seqlen=200, scale=b.scale)
+    torch.cuda.synchronize()
+    kp, vp = _to64(b.k_pool), _to64(b.v_pool)
+    o = _to64(out)
+    for i, r in enumerate(rows):
+        if r == 1:
+            np.testing.assert_array_equal(o[i], 0.0)
+            continue
+        ref = paged_decode_f64(_to64(q)[i:i + 1], kp, vp, [b.tables[r]], [b.lens[r]], 16, b.scale)
+        np.testing.assert_allclose(o[i], ref[0], atol=2e-2, rtol=1e-2)
 
 
 def test_seq_rows_indirection(gpu):
@@ -60,7 +126,7 @@ def test_seq_rows_indirection(gpu):
     rows = [4, 0, 2, 2]
     rows_t = torch.tensor(rows, dtype=torch.int32, device=gpu)
     q = b.q[:4].contiguous()
-    out = ops.paged_decode(q, b.k_pool, b.v_pool, block_tables=b.block_tables, seq_lens=b.seq_lens,
+    out = ops.paged_decode(q, b.k_store, b.v_store, layout=b.layout, block_tables=b.block_tables, seq_lens=b.seq_lens,
                            seq_rows=rows_t, max_seqlen=200, chunk_tokens=32, scale=b.scale)
     torch.cuda.synchronize()
     ref = paged_decode_f64(_to64(q), _to64(b.k_pool), _to64(b.v_pool),
@@ -91,7 +157,7 @@ def test_out_of_range_page_ids_are_masked(gpu):
     b = paged_decode_batch(N=2, Hq=8, Hkv=2, D=64, device=gpu, num_blocks=32, lens=[40, 40], seed=5)
     bad = b.block_tables.clone()
     bad[0, 1] = 10_000_000  # tokens 16..31 of sequence 0
-    out = ops.paged_decode(b.q, b.k_pool, b.v_pool, block_tables=bad, seq_lens=b.seq_lens,
+    out = ops.paged_decode(b.q, b.k_store, b.v_store, layout=b.layout, block_tables=bad, seq_lens=b.seq_lens,
                            max_seqlen=40, scale=b.scale)
     torch.cuda.synchronize()
     kp, vp = _to64(b.k_pool), _to64(b.v_pool)
@@ -106,17 +172,19 @@ def test_out_of_range_page_ids_are_masked(gpu):
 def test_rejects_bad_shapes_on_host(gpu):
     b = paged_decode_batch(N=2, Hq=8, Hkv=2, D=64, device=gpu, num_blocks=16, lens=[10, 20], seed=1)
     with pytest.raises(ValueError):
-        ops.paged_decode(b.q, b.k_pool, b.v_pool, block_tables=b.block_tables, seq_lens=b.seq_lens,
+        ops.paged_decode(b.q, b.k_store, b.v_store, layout=b.layout, block_tables=b.block_tables, seq_lens=b.seq_lens,
                          max_seqlen=10_000)  # table rows too short for max_seqlen
     with pytest.raises(ValueError):
-        ops.paged_decode(b.q.float(), b.k_pool, b.v_pool, block_tables=b.block_tables,
+        ops.paged_decode(b.q.float(), b.k_store, b.v_store, layout=b.layout, block_tables=b.block_tables,
                          seq_lens=b.seq_lens, max_seqlen=20)
 
 
-def test_llama3_8b_shapes_full_size(gpu):
+@pytest.mark.parametrize("layout", [LAYOUT_NATIVE, LAYOUT_REFERENCE])
+def test_llama3_8b_shapes_full_size(gpu, layout):
     """The measured workload at full size (64 seqs, ctx U[512,4096], 64k-page pool)."""
-    b = paged_decode_batch(device=gpu)
-    out = ops.paged_decode(b.q, b.k_pool, b.v_pool, block_tables=b.block_tables, seq_lens=b.seq_lens,
+    print(f"case full size layout={layout}", flush=True)
+    b = paged_decode_batch(device=gpu, layout=layout)
+    out = ops.paged_decode(b.q, b.k_store, b.v_store, layout=b.layout, block_tables=b.block_tables, seq_lens=b.seq_lens,
                            max_seqlen=b.max_seqlen, scale=b.scale)
     torch.cuda.synchronize()
     q64 = _to64(b.q)
