@@ -143,6 +143,42 @@ int mentat_table_copy_rows(int32_t* tables, int32_t* seq_lens, int L, int64_t ro
                            const int32_t* src_rows, const int32_t* dst_rows, int n, int64_t n_entries,
                            void* stream);
 
+/* ------------------------------------------------------------------------
+ * Fused per-row statistics, gate and sampling over [R, V] logits (row_stride
+ * elements apart), one workgroup per row, all outputs device arrays:
+ *   out_entropy[R]      entropy (nats) of softmax(x / temperature), raw logits
+ *                       (compute_entropy at the gate temperature,
+ *                       core/generator_utils.py:196-202, core/generator.py:342)
+ *   out_gate[R]         out_entropy > gate_threshold (may be NULL)
+ *   xp                  repetition penalty over the row's ids in CSR
+ *                       pen_offsets[R+1] / pen_ids (duplicates ignored; NULL or
+ *                       penalty == 1: none), core/generator_utils.py:205-230
+ *   out_entropy_pen[R]  entropy of softmax(xp) (core/generator.py:293; may be NULL)
+ *   out_lse[R]          log-sum-exp of xp (may be NULL)
+ *   out_topk[R,topk], out_topk_lp[R,topk]
+ *                       the topk (0..8) best log_softmax(xp) values in the logits
+ *                       dtype and their ids, ties to the lowest id; topk = 1 is the
+ *                       argmax of core/generator.py:308-310, topk = K the branch
+ *                       children of :283-287
+ *   out_sample[R]       if do_sample: temperature + top-p draw from xp with
+ *                       Philox4x32-10 (key = seed, counter = (row, step, 0)),
+ *                       bit-exact per the oracle's sampling_ref.c; the only
+ *                       temperature/top-p sampling of the reference is HF
+ *                       generate (baseline_rollout.py:56-66)
+ * V <= 524288. dtype: MENTAT_BF16 / MENTAT_F16 / MENTAT_F32.
+ * ---------------------------------------------------------------------- */
+int mentat_row_stats(const void* logits, int64_t row_stride, int R, int V, int dtype, float temperature,
+                     float penalty, const int32_t* pen_offsets, const int32_t* pen_ids,
+                     float gate_threshold, int topk, int do_sample, float sample_temperature,
+                     float top_p, uint64_t seed, uint64_t step, float* out_entropy,
+                     float* out_entropy_pen, float* out_lse, uint8_t* out_gate, int32_t* out_topk,
+                     float* out_topk_lp, int32_t* out_sample, void* stream);
+
+/* Philox4x32-10 blocks: out[4i..4i+3] = rounds(counters[4i..], keys[2i..]) for
+ * i < n (device arrays). The generator mentat_row_stats draws from. */
+int mentat_philox4x32_10(const uint32_t* counters, const uint32_t* keys, uint32_t* out, int n,
+                         void* stream);
+
 #ifdef __cplusplus
 }
 #endif

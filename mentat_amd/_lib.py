@@ -69,6 +69,18 @@ SIGNATURES: dict[str, tuple] = {
         _c_int,
         [_c_void_p, _c_void_p, _c_int, _c_i64, _c_i64, _c_void_p, _c_void_p, _c_int, _c_i64, _c_void_p],
     ),
+    "mentat_row_stats": (
+        _c_int,
+        [
+            _c_void_p, _c_i64, _c_int, _c_int, _c_int, _c_float,  # logits, stride, R, V, dtype, temperature
+            _c_float, _c_void_p, _c_void_p,  # penalty, pen_offsets, pen_ids
+            _c_float, _c_int, _c_int, _c_float,  # gate_threshold, topk, do_sample, sample_temperature
+            _c_float, _c_u64, _c_u64,  # top_p, seed, step
+            _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,  # outputs
+            _c_void_p,  # stream
+        ],
+    ),
+    "mentat_philox4x32_10": (_c_int, [_c_void_p, _c_void_p, _c_void_p, _c_int, _c_void_p]),
 }
 
 LAYOUT_REFERENCE = 0

@@ -1,0 +1,616 @@
+// Fused per-row entropy, gate, repetition penalty, argmax / top-K and
+// temperature + top-p sampling over the full vocabulary (gfx950).
+//
+// One 1024-thread workgroup per logits row. Every pass streams the row with
+// 16-byte loads in the order element = (chunk*1024 + thread)*EPV + e; the first
+// pass reads HBM, later passes are served from the L2 / MALL caches.
+//
+// Per row (reference semantics, cited):
+//   H_T      entropy of softmax(x / T) of the raw logits, in nats
+//            (compute_entropy at the gate temperature, core/generator_utils.py:196-202,
+//            called at core/generator.py:342); fp32 instead of the logits dtype.
+//   gate     H_T > gate_threshold (absolute gate; the relative EMA gate of
+//            core/generator.py:346-369 is applied by the host on H_T).
+//   xp       repetition penalty on the row's generated ids (deduplicated, as the
+//            reference's set(), core/generator_utils.py:205-230):
+//            x > 0 ? x / p : x * p in fp32, rounded to the logits dtype.
+//   keys     log_softmax(xp) as torch forms it: fl(fl(xp - max) - log(sum exp)),
+//            rounded to the logits dtype (core/generator.py:283, :308).
+//   top-K    the K largest keys, ties to the lowest index; argmax = top-1
+//            (torch.argmax's first-occurrence rule; torch.topk leaves tie order
+//            unspecified, this kernel fixes it) and their log-probs = keys.
+//   H_pen    entropy of softmax(xp) at T = 1 (the diagnostic of core/generator.py:293).
+//   sample   temperature + top-p draw from xp with a Philox4x32-10 stream; the
+//            bit-exact specification (deterministic exp2, 2^40 fixed-point masses,
+//            nucleus and inverse-CDF draw) is the oracle's sampling_ref.c.
+#include <utility>
+
+#include "mentat_common.h"
+
+#pragma clang fp contract(off)
+
+namespace mentat {
+
+constexpr int kRowThreads = 1024;
+constexpr int kRowWaves = kRowThreads / 64;
+constexpr int kMaxTopK = 8;
+
+struct RowParams {
+  const void* logits;
+  int64_t row_stride;  // elements
+  int R, V;
+  float ent_c;         // log2(e) / T for the gate entropy
+  float samp_c;        // log2(e) / T for the sampler
+  float penalty;       // 1.0 = off
+  const int32_t* pen_offsets;  // [R+1] or null
+  const int32_t* pen_ids;
+  int topk;
+  uint64_t top_p_q32;  // round(top_p * 2^32)
+  uint64_t seed;
+  uint64_t step;
+  int do_sample;
+  float gate_threshold;
+  float* out_entropy;      // [R]
+  float* out_entropy_pen;  // [R] or null
+  float* out_lse;          // [R] or null (log-sum-exp of xp)
+  uint8_t* out_gate;       // [R] or null
+  int32_t* out_topk;       // [R, topk] or null
+  float* out_topk_lp;      // [R, topk] or null
+  int32_t* out_sample;     // [R] or null
+};
+
+// ---- deterministic exp2 and Philox (must match oracle/csrc/sampling_ref.c) ----------------
+__device__ __forceinline__ float det_exp2(float y) {
+  if (!(y >= -64.0f)) return 0.0f;
+  const float n = rintf(y);
+  const float f = y - n;
+  float p = 0x1.ffcbfcp-17f;
+  p = fmaf(p, f, 0x1.430912p-13f);
+  p = fmaf(p, f, 0x1.5d87fep-10f);
+  p = fmaf(p, f, 0x1.3b2ab6p-7f);
+  p = fmaf(p, f, 0x1.c6b08ep-5f);
+  p = fmaf(p, f, 0x1.ebfbe0p-3f);
+  p = fmaf(p, f, 0x1.62e430p-1f);
+  p = fmaf(p, f, 0x1.000000p+0f);
+  return ldexpf(p, (int)n);
+}
+__device__ __forceinline__ uint64_t det_q(float y) {
+  return (uint64_t)(det_exp2(y) * 0x1p40f);
+}
+__device__ __forceinline__ void philox4x32_10(uint32_t c[4], uint32_t k0, uint32_t k1) {
+_Pragma("clang loop unroll(full)")
+  for (int r = 0; r < 10; ++r) {
+    const uint64_t p0 = (uint64_t)0xD2511F53u * c[0];
+    const uint64_t p1 = (uint64_t)0xCD9E8D57u * c[2];
+    const uint32_t n0 = (uint32_t)(p1 >> 32) ^ c[1] ^ k0;
+    const uint32_t n2 = (uint32_t)(p0 >> 32) ^ c[3] ^ k1;
+    c[1] = (uint32_t)p1;
+    c[3] = (uint32_t)p0;
+    c[0] = n0;
+    c[2] = n2;
+    k0 += 0x9E3779B9u;
+    k1 += 0xBB67AE85u;
+  }
+}
+
+// Compile-time loop: f(std::integral_constant<int, I>) for I = 0 .. N-1.
+template <typename F, int... I>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
+// ---- element access ---------------------------------------------------------------------
+template <typename T> struct RowElem;
+template <> struct RowElem<BF16> {
+  static constexpr int EPV = 8;
+  __device__ static float get(const uint4& w, int e) {
+    const uint32_t d = e < 2 ? w.x : e < 4 ? w.y : e < 6 ? w.z : w.w;
+    return (e & 1) ? bf16_hi(d) : bf16_lo(d);
+  }
+  __device__ static float round(float v) { return __uint_as_float(((uint32_t)f32_to_bf16(v)) << 16); }
+  // Order-preserving 32-bit key of a value of this dtype (only the top 16 bits vary).
+  __device__ static uint32_t key(float v) {
+    const uint32_t u = __float_as_uint(v == 0.f ? 0.f : v);  // -0 and +0 tie, as in float order
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  }
+  __device__ static float scalar(const void* p, long i) { return Elem<BF16>::load1(p, i); }
+  // Radix levels (bits, most significant first) covering the key bits that vary.
+  static constexpr int nlevels = 2;
+  static constexpr int level_bits[3] = {12, 4, 0};
+};
+template <> struct RowElem<F16> {
+  static constexpr int EPV = 8;
+  __device__ static float get(const uint4& w, int e) {
+    const uint32_t d = e < 2 ? w.x : e < 4 ? w.y : e < 6 ? w.z : w.w;
+    return f16_bits_to_f32((uint16_t)((e & 1) ? (d >> 16) : (d & 0xffffu)));
+  }
+  __device__ static float round(float v) { return f16_bits_to_f32(f32_to_f16_bits(v)); }
+  __device__ static uint32_t key(float v) {
+    const uint32_t u = __float_as_uint(v == 0.f ? 0.f : v);  // -0 and +0 tie, as in float order
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  }
+  __device__ static float scalar(const void* p, long i) { return Elem<F16>::load1(p, i); }
+  static constexpr int nlevels = 3;
+  static constexpr int level_bits[3] = {12, 12, 8};
+};
+template <> struct RowElem<F32> {
+  static constexpr int EPV = 4;
+  __device__ static float get(const uint4& w, int e) {
+    return __uint_as_float(e == 0 ? w.x : e == 1 ? w.y : e == 2 ? w.z : w.w);
+  }
+  __device__ static float round(float v) { return v; }
+  __device__ static uint32_t key(float v) {
+    const uint32_t u = __float_as_uint(v == 0.f ? 0.f : v);  // -0 and +0 tie, as in float order
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  }
+  __device__ static float scalar(const void* p, long i) { return ((const float*)p)[i]; }
+  static constexpr int nlevels = 3;
+  static constexpr int level_bits[3] = {12, 12, 8};
+};
+
+// Inverse of RowElem::key: the float whose ordered key is k.
+__device__ __forceinline__ float key_to_float(uint32_t k) {
+  return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
+}
+
+// ---- block reductions (1024 threads) ----------------------------------------------------------
+constexpr int kHistBins = 4096;  // widest radix level: 12 key bits
+
+struct RowShared {
+  float f[kRowWaves * 4];
+  uint64_t u[kRowWaves];
+  uint64_t hist0[kHistBins];  // first radix level (shared by both selections)
+  uint64_t hist1[kHistBins];  // deeper levels
+  uint64_t part[kRowThreads];  // per-thread partial sums for the bin scans
+  uint32_t sel[4];
+  uint64_t sel64[4];
+  float bk[kRowWaves];
+  int32_t bi[kRowWaves];
+  uint32_t chunk_tot[64];
+  int32_t scan[kRowThreads];
+};
+
+__device__ __forceinline__ float wave_max(float v) {
+_Pragma("clang loop unroll(full)")
+  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+  return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+_Pragma("clang loop unroll(full)")
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+__device__ __forceinline__ uint64_t wave_sum_u64(uint64_t v) {
+_Pragma("clang loop unroll(full)")
+  for (int o = 32; o >= 1; o >>= 1) {
+    const uint32_t lo = __shfl_xor((uint32_t)v, o), hi = __shfl_xor((uint32_t)(v >> 32), o);
+    v += ((uint64_t)hi << 32) | lo;
+  }
+  return v;
+}
+
+// Reduce up to 4 floats at once: op 0 = max, 1 = sum (per value).
+template <int NVAL>
+__device__ __forceinline__ void block_reduce(float (&v)[NVAL], const int (&op)[NVAL], RowShared& sh) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+_Pragma("clang loop unroll(full)")
+  for (int i = 0; i < NVAL; ++i) v[i] = op[i] == 0 ? wave_max(v[i]) : wave_sum(v[i]);
+  __syncthreads();
+  if (lane == 0) {
+_Pragma("clang loop unroll(full)")
+    for (int i = 0; i < NVAL; ++i) sh.f[wave * 4 + i] = v[i];
+  }
+  __syncthreads();
+_Pragma("clang loop unroll(full)")
+  for (int i = 0; i < NVAL; ++i) {
+    float a = op[i] == 0 ? kNegInf : 0.f;
+    for (int w = 0; w < kRowWaves; ++w) a = op[i] == 0 ? fmaxf(a, sh.f[w * 4 + i]) : a + sh.f[w * 4 + i];
+    v[i] = a;
+  }
+}
+__device__ __forceinline__ uint64_t block_sum_u64(uint64_t v, RowShared& sh) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  v = wave_sum_u64(v);
+  __syncthreads();
+  if (lane == 0) sh.u[wave] = v;
+  __syncthreads();
+  uint64_t a = 0;
+  for (int w = 0; w < kRowWaves; ++w) a += sh.u[w];
+  return a;
+}
+
+// (key, idx) ordering for top-K: larger key first, then lower index.
+__device__ __forceinline__ bool tk_better(float ka, int ia, float kb, int ib) {
+  return ka > kb || (ka == kb && ia < ib);
+}
+// Insert (key, idx) into a sorted top-8 list, dropping the worst; every index is
+// static (the carried element is swapped down the list).
+__device__ __forceinline__ void tk_insert(float (&k)[kMaxTopK], int (&ix)[kMaxTopK], float key, int idx) {
+  if (!tk_better(key, idx, k[kMaxTopK - 1], ix[kMaxTopK - 1])) return;
+_Pragma("clang loop unroll(full)")
+  for (int j = 0; j < kMaxTopK; ++j) {
+    if (tk_better(key, idx, k[j], ix[j])) {
+      const float tkk = k[j];
+      const int tii = ix[j];
+      k[j] = key;
+      ix[j] = idx;
+      key = tkk;
+      idx = tii;
+    }
+  }
+}
+
+// Stream the row in steps of four chunks (four 16-byte loads in flight per
+// thread); the body sees `c` (chunk) and `x` (its EPV elements). Expanded in
+// place so that accumulators stay in registers.
+#define ROW_FOR_GROUPS(...)                                              \
+  for (int c0_ = 0; c0_ < nchunks; c0_ += 4) {                           \
+    float xg_[4][EPV];                                                   \
+    _Pragma("clang loop unroll(full)") for (int u_ = 0; u_ < 4; ++u_)                     \
+      if (c0_ + u_ < nchunks) load_group(c0_ + u_, xg_[u_]);             \
+    _Pragma("clang loop unroll(full)") for (int u_ = 0; u_ < 4; ++u_) {                   \
+      if (c0_ + u_ < nchunks) {                                          \
+        const int c = c0_ + u_;                                          \
+        float(&x)[EPV] = xg_[u_];                                        \
+        __VA_ARGS__                                                      \
+      }                                                                  \
+    }                                                                    \
+  }
+
+constexpr int kMaxChunks = 64;                              // chunks of 1024 x EPV elements
+constexpr int kMaxPenWords = kMaxChunks * kRowThreads * 8 / 32;  // penalty bits (V <= 524288)
+
+template <typename T>
+__global__ __launch_bounds__(kRowThreads) void row_stats_kernel(RowParams p) {
+  using RE = RowElem<T>;
+  using S = typename T::storage;
+  constexpr int EPV = RE::EPV;
+  const int row = blockIdx.x;
+  if (row >= p.R) return;
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63;
+  __shared__ RowShared sh;
+  __shared__ uint32_t pbits[kMaxPenWords];
+  const char* rp = (const char*)p.logits + (long)row * p.row_stride * (long)sizeof(S);
+  const int nchunks = (p.V + kRowThreads * EPV - 1) / (kRowThreads * EPV);
+
+  // Elements e of this thread's 16-byte group in chunk c (-inf past the end);
+  // rows that do not start on a 16-byte boundary are read element by element.
+  const bool aligned = (((uintptr_t)rp) & 15u) == 0;
+  auto load_group = [&](int c, float (&x)[EPV]) __attribute__((always_inline)) {
+    const int i0 = (c * kRowThreads + tid) * EPV;
+    if (aligned && i0 + EPV <= p.V) {
+      const uint4 w = *(const uint4*)(rp + (long)i0 * sizeof(S));
+_Pragma("clang loop unroll(full)")
+      for (int e = 0; e < EPV; ++e) x[e] = RE::get(w, e);
+    } else {
+_Pragma("clang loop unroll(full)")
+      for (int e = 0; e < EPV; ++e) x[e] = (i0 + e < p.V) ? RE::scalar(rp, i0 + e) : kNegInf;
+    }
+  };
+
+  // ---- repetition-penalty bitmask ----
+  const int nwords = (p.V + 31) / 32;
+  const bool use_pen = p.penalty != 1.0f && p.pen_offsets != nullptr;
+  if (use_pen) {
+    for (int w = tid; w < nwords; w += kRowThreads) pbits[w] = 0u;
+    __syncthreads();
+    const int b = p.pen_offsets[row], e = p.pen_offsets[row + 1];
+    for (int j = b + tid; j < e; j += kRowThreads) {
+      const int id = p.pen_ids[j];
+      if (id >= 0 && id < p.V) atomicOr(&pbits[id >> 5], 1u << (id & 31));
+    }
+    __syncthreads();
+  }
+  auto penal = [&](int i, float x) __attribute__((always_inline)) -> float {
+    if (!use_pen || i >= p.V || !((pbits[i >> 5] >> (i & 31)) & 1u)) return x;
+    return RE::round(x > 0.f ? __fdiv_rn(x, p.penalty) : x * p.penalty);
+  };
+
+  // ---- pass 1: maxima of x and xp ----
+  float mx[2] = {kNegInf, kNegInf};
+  ROW_FOR_GROUPS(
+    const int i0 = (c * kRowThreads + tid) * EPV;
+    static_for<EPV>([&](auto ec_) __attribute__((always_inline)) {
+      constexpr int e = decltype(ec_)::value;
+      mx[0] = fmaxf(mx[0], x[e]);
+      mx[1] = fmaxf(mx[1], penal(i0 + e, x[e]));
+        });
+    )
+  { const int op[2] = {0, 0}; block_reduce<2>(mx, op, sh); }
+  const float m_raw = mx[0], m_pen = mx[1];
+
+  // ---- pass 2: entropy sums (base 2) and fixed-point sampling masses ----
+  // The T = 1 sums of xp feed the top-K keys, the log-sum-exp and H_pen only.
+  const bool need_pen_sums = p.topk > 0 || p.out_entropy_pen != nullptr || p.out_lse != nullptr;
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  uint64_t zq = 0;
+  ROW_FOR_GROUPS(
+    const int i0 = (c * kRowThreads + tid) * EPV;
+    static_for<EPV>([&](auto ec_) __attribute__((always_inline)) {
+      constexpr int e = decltype(ec_)::value;
+      if (i0 + e >= p.V) return;
+      const float y = (x[e] - m_raw) * p.ent_c;
+      const float ey = fast_exp2(y);
+      acc[0] += ey;
+      acc[1] += ey > 0.f ? ey * y : 0.f;
+      const float xp = penal(i0 + e, x[e]);
+      if (need_pen_sums) {
+        const float y1 = (xp - m_pen) * kLog2e;
+        const float e1 = fast_exp2(y1);
+        acc[2] += e1;
+        acc[3] += e1 > 0.f ? e1 * y1 : 0.f;
+      }
+      if (p.do_sample) zq += det_q((xp - m_pen) * p.samp_c);
+        });
+    )
+  { const int op[4] = {1, 1, 1, 1}; block_reduce<4>(acc, op, sh); }
+  const float H_T = (log2f(acc[0]) - acc[1] / acc[0]) * kLn2;
+  const float H_pen = (log2f(acc[2]) - acc[3] / acc[2]) * kLn2;
+  const float logsum = logf(acc[2]);  // ln(sum exp(xp - max)), as log_softmax forms it
+  if (tid == 0) {
+    p.out_entropy[row] = H_T;
+    if (p.out_entropy_pen) p.out_entropy_pen[row] = H_pen;  // NaN-free only when computed
+    if (p.out_lse) p.out_lse[row] = m_pen + logsum;
+    if (p.out_gate) p.out_gate[row] = H_T > p.gate_threshold ? 1 : 0;
+  }
+
+  // ---- pass 3: top-K of the log-softmax keys ----
+  // K passes; pass j takes the best (key desc, index asc) element strictly after
+  // the (j-1)-th pick, so every pass is a plain compare-and-select per element.
+  if (p.topk > 0) {
+    float prev_k = __builtin_huge_valf();
+    int prev_i = -1;
+    for (int j = 0; j < p.topk; ++j) {
+      float bk = kNegInf;
+      int bi = 0x7fffffff;
+      ROW_FOR_GROUPS(
+        const int i0 = (c * kRowThreads + tid) * EPV;
+        static_for<EPV>([&](auto ec_) __attribute__((always_inline)) {
+          constexpr int e = decltype(ec_)::value;
+          const int i = i0 + e;
+          if (i >= p.V) return;
+          const float key = RE::round((penal(i, x[e]) - m_pen) - logsum);
+          const bool after = key < prev_k || (key == prev_k && i > prev_i);
+          if (after && tk_better(key, i, bk, bi)) { bk = key; bi = i; }
+                });
+      )
+      for (int o = 32; o >= 1; o >>= 1) {
+        const float ok = __shfl_xor(bk, o);
+        const int oi = __shfl_xor(bi, o);
+        if (tk_better(ok, oi, bk, bi)) { bk = ok; bi = oi; }
+      }
+      __syncthreads();
+      if (lane == 0) { sh.bk[wave] = bk; sh.bi[wave] = bi; }
+      __syncthreads();
+      bk = sh.bk[0];
+      bi = sh.bi[0];
+      for (int w = 1; w < kRowWaves; ++w)
+        if (tk_better(sh.bk[w], sh.bi[w], bk, bi)) { bk = sh.bk[w]; bi = sh.bi[w]; }
+      if (tid == 0) {
+        if (p.out_topk) p.out_topk[(long)row * p.topk + j] = bi;
+        if (p.out_topk_lp) p.out_topk_lp[(long)row * p.topk + j] = bk;
+      }
+      prev_k = bk;
+      prev_i = bi;
+    }
+  }
+
+  // ---- pass 4: exact temperature + top-p draw ----
+  if (!p.do_sample) return;
+  const uint64_t Z = block_sum_u64(zq, sh);
+  uint64_t need = (uint64_t)(((unsigned __int128)Z * p.top_p_q32 + 0xffffffffull) >> 32);
+  if (need < 1) need = 1;
+  constexpr int NLEV = RE::nlevels;
+
+  // Histogram of masses by the `bits` key bits below `done` already-fixed bits
+  // equal to `prefix`, into h (bins = 1 << bits).
+  auto histogram = [&](uint64_t* h, int done, uint32_t prefix, int bits) __attribute__((always_inline)) {
+    const int nb = 1 << bits;
+    for (int t = tid; t < nb; t += kRowThreads) h[t] = 0;
+    __syncthreads();
+    const int shift = 32 - done - bits;
+    ROW_FOR_GROUPS(
+      const int i0 = (c * kRowThreads + tid) * EPV;
+      static_for<EPV>([&](auto ec_) __attribute__((always_inline)) {
+        constexpr int e = decltype(ec_)::value;
+        if (i0 + e >= p.V) return;
+        const float xp = penal(i0 + e, x[e]);
+        const uint32_t k = RE::key(xp);
+        if (done > 0 && (k >> (32 - done)) != prefix) return;
+        const uint64_t q = det_q((xp - m_pen) * p.samp_c);
+        if (q) atomicAdd((unsigned long long*)&h[(k >> shift) & (uint32_t)(nb - 1)], (unsigned long long)q);
+            });
+    )
+    __syncthreads();
+  };
+  // Bin b of h (largest bins first) with above + mass(bins > b) <= pos < above + mass(bins >= b);
+  // returns b and adds mass(bins > b) to above.
+  auto pick_bin = [&](const uint64_t* h, int bits, uint64_t pos, uint64_t& above) __attribute__((always_inline)) -> uint32_t {
+    const int nb = 1 << bits;
+    const int per = (nb + kRowThreads - 1) / kRowThreads;  // bins per thread, top-down
+    // thread t owns bins nb-1-t*per ... nb-1-(t*per+per-1)
+    uint64_t mine = 0;
+    for (int j = 0; j < per; ++j) {
+      const int b = nb - 1 - (tid * per + j);
+      if (b >= 0) mine += h[b];
+    }
+    sh.part[tid] = mine;
+    __syncthreads();
+    for (int off = 1; off < kRowThreads; off <<= 1) {
+      const uint64_t v = tid >= off ? sh.part[tid - off] : 0;
+      __syncthreads();
+      sh.part[tid] += v;
+      __syncthreads();
+    }
+    uint64_t run = above + sh.part[tid] - mine;  // mass of all bins above this thread's
+    for (int j = 0; j < per; ++j) {
+      const int b = nb - 1 - (tid * per + j);
+      if (b < 0) break;
+      if (h[b] != 0 && run <= pos && pos < run + h[b]) {
+        sh.sel[0] = (uint32_t)b;
+        sh.sel64[0] = run;
+      }
+      run += h[b];
+    }
+    __syncthreads();
+    const uint32_t b = sh.sel[0];
+    above = sh.sel64[0];
+    __syncthreads();
+    return b;
+  };
+  // Key holding mass position pos (order: xp desc, index asc) and the mass above it.
+  auto select = [&](uint64_t pos, uint32_t& key_out, uint64_t& above_out) __attribute__((always_inline)) {
+    uint64_t above = 0;
+    uint32_t prefix = pick_bin(sh.hist0, RE::level_bits[0], pos, above);
+    int done = RE::level_bits[0];
+    _Pragma("clang loop unroll(full)")
+    for (int lev = 1; lev < NLEV; ++lev) {
+      const int bits = RE::level_bits[lev];
+      histogram(sh.hist1, done, prefix, bits);
+      prefix = (prefix << bits) | pick_bin(sh.hist1, bits, pos, above);
+      done += bits;
+    }
+    key_out = prefix << (32 - done);  // the full 32-bit key (low bits zero for bf16)
+    above_out = above;
+  };
+  constexpr int kKeyBitsUsed = RE::level_bits[0] + RE::level_bits[1] + RE::level_bits[2];
+  auto match = [&](float xp, uint32_t kk) {
+    return (RE::key(xp) >> (32 - kKeyBitsUsed)) == (kk >> (32 - kKeyBitsUsed));
+  };
+  // Mass of one token with key kk (every such token has the value key_to_float(kk)).
+  auto key_mass = [&](uint32_t kk) -> uint64_t { return det_q((key_to_float(kk) - m_pen) * p.samp_c); };
+
+  histogram(sh.hist0, 0, 0u, RE::level_bits[0]);
+  uint32_t key_n;
+  uint64_t above_n;
+  select(need - 1, key_n, above_n);
+  const uint64_t qn = key_mass(key_n);
+  const uint64_t jn = (need - 1 - above_n) / qn;  // 0-based index of the last kept tie
+  const uint64_t kept_mass = above_n + (jn + 1) * qn;
+
+  uint32_t c4[4] = {(uint32_t)row, (uint32_t)p.step, (uint32_t)(p.step >> 32), 0u};
+  philox4x32_10(c4, (uint32_t)p.seed, (uint32_t)(p.seed >> 32));
+  const uint64_t U = ((uint64_t)c4[0] << 32) | c4[1];
+  const uint64_t r = (uint64_t)(((unsigned __int128)U * kept_mass) >> 64);
+
+  uint32_t key_r;
+  uint64_t above_r;
+  select(r, key_r, above_r);
+  const uint64_t qr = key_mass(key_r);
+  const uint32_t j = (uint32_t)((r - above_r) / qr);  // the j-th (0-based) token of key_r by index
+
+  // The j-th token with key_r in index order: per-chunk totals, then a thread scan.
+  if (tid < kMaxChunks) sh.chunk_tot[tid] = 0;
+  __syncthreads();
+  ROW_FOR_GROUPS(
+    const int i0 = (c * kRowThreads + tid) * EPV;
+    uint32_t n = 0;
+_Pragma("clang loop unroll(full)")
+    for (int e = 0; e < EPV; ++e)
+      if (i0 + e < p.V && match(penal(i0 + e, x[e]), key_r)) ++n;
+    for (int o = 32; o >= 1; o >>= 1) n += __shfl_xor(n, o);
+    if (lane == 0 && n) atomicAdd(&sh.chunk_tot[c], n);
+    )
+  __syncthreads();
+  int cstar = 0;
+  uint32_t before = 0;
+  for (int c = 0; c < nchunks; ++c) {
+    if (before + sh.chunk_tot[c] > j) { cstar = c; break; }
+    before += sh.chunk_tot[c];
+  }
+  float xs[EPV];
+  load_group(cstar, xs);
+  const int is0 = (cstar * kRowThreads + tid) * EPV;
+  uint32_t mine = 0;
+_Pragma("clang loop unroll(full)")
+  for (int e = 0; e < EPV; ++e)
+    if (is0 + e < p.V && match(penal(is0 + e, xs[e]), key_r)) ++mine;
+  sh.scan[tid] = (int32_t)mine;
+  __syncthreads();
+  for (int off = 1; off < kRowThreads; off <<= 1) {
+    const int32_t v = tid >= off ? sh.scan[tid - off] : 0;
+    __syncthreads();
+    sh.scan[tid] += v;
+    __syncthreads();
+  }
+  const uint32_t excl = before + (uint32_t)sh.scan[tid] - mine;
+  if (mine && excl <= j && j < excl + mine) {
+    uint32_t seen = excl;
+    static_for<EPV>([&](auto ec_) __attribute__((always_inline)) {
+      constexpr int e = decltype(ec_)::value;
+      if (is0 + e < p.V && match(penal(is0 + e, xs[e]), key_r)) {
+        if (seen == j && p.out_sample) p.out_sample[row] = is0 + e;
+        ++seen;
+      }
+        });
+  }
+}
+
+template <typename T>
+static int dispatch_rows(const RowParams& p, hipStream_t s) {
+  constexpr int EPV = RowElem<T>::EPV;
+  const long nchunks = ((long)p.V + kRowThreads * EPV - 1) / (kRowThreads * EPV);
+  if (nchunks > kMaxChunks || (long)p.V > (long)kMaxPenWords * 32) return MENTAT_EUNSUP;
+  hipLaunchKernelGGL((row_stats_kernel<T>), dim3(p.R), dim3(kRowThreads), 0, s, p);
+  return (int)hipGetLastError();
+}
+
+}  // namespace mentat
+
+using namespace mentat;
+
+extern "C" int mentat_row_stats(const void* logits, int64_t row_stride, int R, int V, int dtype,
+                                float temperature, float penalty, const int32_t* pen_offsets,
+                                const int32_t* pen_ids, float gate_threshold, int topk, int do_sample,
+                                float sample_temperature, float top_p, uint64_t seed, uint64_t step,
+                                float* out_entropy, float* out_entropy_pen, float* out_lse,
+                                uint8_t* out_gate, int32_t* out_topk, float* out_topk_lp,
+                                int32_t* out_sample, void* stream) {
+  if (R == 0) return MENTAT_OK;
+  if (!logits || R < 0 || V <= 0 || row_stride < V || !out_entropy) return MENTAT_EINVAL;
+  if (!(temperature > 0.f) || topk < 0 || topk > kMaxTopK || topk > V) return MENTAT_EINVAL;
+  if (do_sample && (!(sample_temperature > 0.f) || !(top_p > 0.f) || top_p > 1.f || !out_sample))
+    return MENTAT_EINVAL;
+  if (R > 2147483647 / 2) return MENTAT_EINVAL;
+  RowParams p;
+  p.logits = logits; p.row_stride = row_stride; p.R = R; p.V = V;
+  p.ent_c = (float)(1.4426950408889634 / (double)temperature);
+  p.samp_c = do_sample ? (float)(1.4426950408889634 / (double)sample_temperature) : 0.f;
+  p.penalty = penalty; p.pen_offsets = pen_offsets; p.pen_ids = pen_ids;
+  p.topk = topk;
+  p.top_p_q32 = (uint64_t)llrint((double)top_p * 4294967296.0);
+  p.seed = seed; p.step = step; p.do_sample = do_sample; p.gate_threshold = gate_threshold;
+  p.out_entropy = out_entropy; p.out_entropy_pen = out_entropy_pen; p.out_lse = out_lse;
+  p.out_gate = out_gate; p.out_topk = out_topk; p.out_topk_lp = out_topk_lp; p.out_sample = out_sample;
+  hipStream_t s = (hipStream_t)stream;
+  switch (dtype) {
+    case MENTAT_BF16: return dispatch_rows<BF16>(p, s);
+    case MENTAT_F16: return dispatch_rows<F16>(p, s);
+    case MENTAT_F32: return dispatch_rows<F32>(p, s);
+    default: return MENTAT_EUNSUP;
+  }
+}
+
+namespace mentat {
+__global__ void philox_kernel(const uint32_t* counters, const uint32_t* keys, uint32_t* out, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  uint32_t c[4] = {counters[4 * i], counters[4 * i + 1], counters[4 * i + 2], counters[4 * i + 3]};
+  philox4x32_10(c, keys[2 * i], keys[2 * i + 1]);
+  for (int j = 0; j < 4; ++j) out[4 * i + j] = c[j];
+}
+}  // namespace mentat
+
+extern "C" int mentat_philox4x32_10(const uint32_t* counters, const uint32_t* keys, uint32_t* out, int n,
+                                    void* stream) {
+  if (n == 0) return MENTAT_OK;
+  if (!counters || !keys || !out || n < 0) return MENTAT_EINVAL;
+  hipLaunchKernelGGL(philox_kernel, dim3((n + 255) / 256), dim3(256), 0, (hipStream_t)stream, counters, keys,
+                     out, n);
+  return (int)hipGetLastError();
+}

@@ -7,6 +7,7 @@ calls the library on torch's current stream.
 from __future__ import annotations
 
 import math
+from dataclasses import dataclass
 from typing import Optional
 
 import torch
@@ -27,6 +28,9 @@ __all__ = [
     "kv_append",
     "page_copy",
     "table_copy_rows",
+    "row_stats",
+    "RowStats",
+    "philox4x32_10",
     "MentatError",
     "workspace",
     "LAYOUT_NATIVE",
@@ -264,3 +268,90 @@ def table_copy_rows(tables: torch.Tensor, seq_lens: Optional[torch.Tensor], src_
     st = get_lib().mentat_table_copy_rows(ptr(tables), ptr(seq_lens), L, rows, stride, ptr(src_rows),
                                           ptr(dst_rows), src_rows.numel(), n_entries, stream_handle(dev))
     check(st, "mentat_table_copy_rows")
+
+
+@dataclass
+class RowStats:
+    entropy: torch.Tensor                 # [R] f32, entropy of softmax(x / T)
+    gate: torch.Tensor                    # [R] u8, entropy > gate_threshold
+    entropy_pen: Optional[torch.Tensor]   # [R] f32, entropy of softmax(xp)
+    lse: Optional[torch.Tensor]           # [R] f32, log-sum-exp of xp
+    topk_ids: Optional[torch.Tensor]      # [R, K] i32
+    topk_lp: Optional[torch.Tensor]       # [R, K] f32
+    sample: Optional[torch.Tensor]        # [R] i32
+
+
+def row_stats(
+    logits: torch.Tensor,
+    *,
+    temperature: float = 1.0,
+    penalty: float = 1.0,
+    pen_offsets: Optional[torch.Tensor] = None,
+    pen_ids: Optional[torch.Tensor] = None,
+    gate_threshold: float = float("inf"),
+    topk: int = 0,
+    sample: bool = False,
+    sample_temperature: float = 1.0,
+    top_p: float = 1.0,
+    seed: int = 0,
+    step: int = 0,
+    pen_stats: Optional[bool] = None,
+) -> RowStats:
+    """Fused per-row entropy, gate, repetition penalty, top-K and top-p draw
+    (mentat_row_stats in include/mentat_capi.h) over logits [R, V].
+
+    ``pen_stats`` (default: ``topk > 0``) also returns the entropy and
+    log-sum-exp of the penalised row (``entropy_pen``, ``lse``; None otherwise).
+    """
+    if pen_stats is None:
+        pen_stats = topk > 0
+    _require(logits.dim() == 2, "logits must be [R, V]")
+    dev = logits.device
+    _require(dev.type == "cuda", "row_stats runs on the GPU only")
+    _require(logits.dtype in DTYPE_CODES, f"unsupported dtype {logits.dtype}")
+    _require(logits.stride(1) == 1, "logits rows must be contiguous")
+    R, V = logits.shape
+    _require(0 <= topk <= 8, "topk must be in [0, 8]")
+    _require(topk <= V, "topk larger than the vocabulary")
+    _require(temperature > 0, "temperature must be > 0")
+    if pen_offsets is not None:
+        _check_i32(pen_offsets, "pen_offsets", dev)
+        _check_i32(pen_ids, "pen_ids", dev)
+        _require(pen_offsets.numel() == R + 1, "pen_offsets must have R+1 entries")
+    if sample:
+        _require(sample_temperature > 0 and 0 < top_p <= 1, "bad sampling parameters")
+    f32 = dict(dtype=torch.float32, device=dev)
+    out = RowStats(
+        entropy=torch.empty(R, **f32),
+        gate=torch.empty(R, dtype=torch.uint8, device=dev),
+        entropy_pen=torch.empty(R, **f32) if pen_stats else None,
+        lse=torch.empty(R, **f32) if pen_stats else None,
+        topk_ids=torch.empty(R, topk, dtype=torch.int32, device=dev) if topk else None,
+        topk_lp=torch.empty(R, topk, **f32) if topk else None,
+        sample=torch.full((R,), -1, dtype=torch.int32, device=dev) if sample else None,
+    )
+    if R == 0:
+        return out
+    st = get_lib().mentat_row_stats(
+        ptr(logits), logits.stride(0), R, V, DTYPE_CODES[logits.dtype], float(temperature),
+        float(penalty), ptr(pen_offsets), ptr(pen_ids),
+        float(gate_threshold), int(topk), int(bool(sample)), float(sample_temperature),
+        float(top_p), int(seed) & (2**64 - 1), int(step) & (2**64 - 1),
+        ptr(out.entropy), ptr(out.entropy_pen), ptr(out.lse), ptr(out.gate),
+        ptr(out.topk_ids), ptr(out.topk_lp), ptr(out.sample), stream_handle(dev),
+    )
+    check(st, "mentat_row_stats")
+    return out
+
+
+def philox4x32_10(counters: torch.Tensor, keys: torch.Tensor) -> torch.Tensor:
+    """Philox4x32-10 blocks on the device: counters int32/uint32 [n, 4], keys [n, 2]."""
+    dev = counters.device
+    _require(counters.dim() == 2 and counters.shape[1] == 4, "counters must be [n, 4]")
+    _require(keys.shape == (counters.shape[0], 2), "keys must be [n, 2]")
+    c = counters.contiguous().to(torch.int32)
+    k = keys.contiguous().to(torch.int32)
+    out = torch.empty_like(c)
+    st = get_lib().mentat_philox4x32_10(ptr(c), ptr(k), ptr(out), c.shape[0], stream_handle(dev))
+    check(st, "mentat_philox4x32_10")
+    return out

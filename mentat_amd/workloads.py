@@ -130,3 +130,21 @@ def paged_decode_batch(
         block_size=block_size,
         scale=1.0 / float(np.sqrt(D)),
     )
+
+
+def sampling_logits(*, R: int = 256, V: int = 151936, sigma_lo: float = 0.5, sigma_hi: float = 4.0,
+                    dtype: torch.dtype = torch.bfloat16, device: str | torch.device = "cuda",
+                    seed: int = 0):
+    """Logits for the fused entropy-gate + sampling step: row r is sigma_r * N(0, 1)
+    with sigma_r uniform in [sigma_lo, sigma_hi] (seeded), so entropies at
+    T = 0.7 span a 3-nat gate. Returns (logits [R, V], sigmas)."""
+    rng = np.random.default_rng(seed)
+    sig = rng.uniform(sigma_lo, sigma_hi, size=R).astype(np.float32)
+    g = torch.Generator(device=device)
+    g.manual_seed(seed)
+    x = torch.empty(R, V, device=device, dtype=dtype)
+    for r0 in range(0, R, 16):
+        r1 = min(R, r0 + 16)
+        z = torch.randn(r1 - r0, V, generator=g, device=device)
+        x[r0:r1] = (z * torch.from_numpy(sig[r0:r1]).to(device)[:, None]).to(dtype)
+    return x, sig
