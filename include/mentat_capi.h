@@ -102,6 +102,36 @@ int mentat_paged_decode(int layout, const void* q, const void* k_cache, const vo
 int mentat_paged_decode_auto_chunk(int N, int Hkv, int block_size, int max_seqlen);
 
 /* ------------------------------------------------------------------------
+ * Prefix-tree decode attention: the same result as mentat_paged_decode for
+ * every query (core/paged_kv_cache.py:289-368 + adapters/attention_backend.py:
+ * 192-229: query i attends to all of its cached tokens), computed so that a
+ * page shared by several sequences of a branching tree (fork_sequence,
+ * core/paged_kv_cache.py:152-170) is read from HBM once for all of them.
+ * Native pool layout only (K [blk][Hkv][B][D], V [blk][Hkv][D][B]),
+ * bf16/f16, block_size 16/32/64, Hq/Hkv in {1,2,4,8,16}, D in {64,128}.
+ *
+ * The host plan (built once per decode step, shared by all layers):
+ *   items[n_items][24] int32, one per (segment chunk, kv head, member group):
+ *     [0] table row whose ids the chunk reads; [1] first 16-token tile;
+ *     [2] tile count; [3] tokens of the segment (exclusive end, absolute);
+ *     [4] kv head; [5] member count m (<= 16/(Hq/Hkv)); [6] first partial
+ *     slot (member j writes slot [6]+j); [7..7+m) member query indices.
+ *     Items with [2] == 0 are padding.
+ *   q_slot_offsets[Nq*Hkv+1], q_slots[]: the partial slots of (query, kv head)
+ *     q*Hkv+h, merged with the log-sum-exp rule into out.
+ * block_tables: [rows, table_stride] int32 (one layer). Workspace:
+ * mentat_tree_decode_workspace_bytes(n_slots, ...) bytes. Page ids outside
+ * [0, num_blocks) are masked, not read.
+ * ---------------------------------------------------------------------- */
+size_t mentat_tree_decode_workspace_bytes(int n_slots, int Hq, int Hkv, int D);
+
+int mentat_tree_decode(const void* q, const void* k_store, const void* v_store, const int32_t* block_tables,
+                       int64_t table_stride, int64_t num_blocks, const int32_t* items, int n_items,
+                       const int32_t* q_slot_offsets, const int32_t* q_slots, int n_slots, void* out,
+                       int Nq, int Hq, int Hkv, int D, int block_size, float scale, int dtype,
+                       void* workspace, size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------
  * KV append: write n new token rows into the pools, fused with the lazy
  * copy-on-write of a shared tail page and the device block-table update.
  *

@@ -1,0 +1,328 @@
+// Prefix-tree (shared-prefix) decode attention on MFMA (gfx950), native pool layout.
+//
+// Same result as paged decode for every query (sequence i attends to all of its
+// cached tokens, core/paged_kv_cache.py:289-368 + adapters/attention_backend.py:192-229),
+// but pages shared by several sequences of a branching tree are read once for
+// all of them. The host plan splits the batch's contexts into segments: a run
+// of 16-token tiles whose block ids are identical for a set of member queries
+// (the shared prefix, internal tree edges, each leaf's private tail). A work
+// item is (segment chunk, kv head, member group): up to 16/G member queries,
+// i.e. one 16-column MFMA query tile (G = Hq/Hkv query heads per member).
+// The host puts the member groups of one (chunk, head) next to each other; the
+// wavefronts of a workgroup take consecutive items, so the groups of a shared
+// chunk run on one CU and re-read its pages from that CU's caches, not HBM.
+//
+// Per item the wavefront runs the paged_decode_mfma tile loop
+// (S^T = K.Q^T on v_mfma 16x16x32, online softmax, O += P.V on 16x16x16) over
+// the chunk and writes each member's partial (m, l, O) to its slot; a merge
+// kernel combines every query's partials (the LSE rule) into the output.
+#include "mentat_common.h"
+
+namespace mentat {
+
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+template <typename T> struct TMfma;
+template <> struct TMfma<BF16> {
+  __device__ static f32x4_t qk(const uint4& a, const uint4& b, f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                   __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+  }
+  __device__ static f32x4_t pv(const uint2& a, const uint2& b, f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4_t, a),
+                                                     __builtin_bit_cast(s16x4_t, b), c, 0, 0, 0);
+  }
+  __device__ static uint2 pack(f32x4_t v) { return __builtin_bit_cast(uint2, __builtin_convertvector(v, bf16x4_t)); }
+};
+template <> struct TMfma<F16> {
+  __device__ static f32x4_t qk(const uint4& a, const uint4& b, f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a),
+                                                  __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
+  }
+  __device__ static f32x4_t pv(const uint2& a, const uint2& b, f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4_t, a),
+                                                 __builtin_bit_cast(f16x4_t, b), c, 0, 0, 0);
+  }
+  __device__ static uint2 pack(f32x4_t v) { return __builtin_bit_cast(uint2, __builtin_convertvector(v, f16x4_t)); }
+};
+
+// Work item (int32 x kItemFields):
+//   [0] table row whose page ids the chunk reads   [1] first tile   [2] tile count
+//   [3] valid tokens: the chunk covers tokens [16*first, min(16*(first+count), valid))
+//   [4] kv head   [5] members (1 .. 16/G)   [6] first partial slot (member j -> slot + j)
+//   [7 ..] member query indices (kItemFields - 7 of them)
+constexpr int kItemFields = 24;
+constexpr int kItemMembers = kItemFields - 7;
+
+struct TreeParams {
+  const void* q;       // [Nq, Hq, D]
+  const void* k;       // native K store [num_blocks][Hkv][B][D]
+  const void* v;       // native V store [num_blocks][Hkv][D][B]
+  const int32_t* tables;
+  int64_t table_stride;
+  int64_t num_blocks;
+  const int32_t* items;
+  int n_items;
+  float* ws_o;         // [slots][G][D]
+  float* ws_ml;        // [slots][G][2]
+  // merge
+  const int32_t* q_slot_off;  // [Nq*Hkv + 1]: partial slots of (query, kv head)
+  const int32_t* q_slots;
+  void* out;           // [Nq, Hq, D]
+  int Nq, Hq, Hkv, B;
+  float scale_log2;
+};
+
+constexpr int kTreeThreads = 512;  // 8 wavefronts
+constexpr float kTreeSlack = 8.f;
+
+typedef const int32_t __attribute__((address_space(4)))* tconst_i32;
+__device__ __forceinline__ int32_t tld(const int32_t* p, long i) { return ((tconst_i32)p)[i]; }
+__device__ __forceinline__ int tuni(int v) { return __builtin_amdgcn_readfirstlane(v); }
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t trsrc(const void* base, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes, 0x00020000);
+}
+
+template <typename T, int D, int G, int B>
+__global__ __launch_bounds__(kTreeThreads) void tree_decode_kernel(TreeParams p) {
+  constexpr int KS = D / 32, NT = D / 16, NSUB = B / 16, MG = 16 / G;
+  using S = typename T::storage;
+  const int lane = threadIdx.x & 63;
+  const int it = tuni(blockIdx.x * (kTreeThreads / 64) + (threadIdx.x >> 6));
+  if (it >= p.n_items) return;
+  const int32_t* item = p.items + (long)it * kItemFields;
+  const int row = tld(item, 0), t_first = tld(item, 1), ntile = tld(item, 2), valid = tld(item, 3);
+  const int head = tld(item, 4), nmem = tld(item, 5), slot0 = tld(item, 6);
+  if (ntile <= 0 || nmem <= 0) return;
+  const int t_last = t_first + ntile;
+  const int lr = lane & 15, lg = lane >> 4;
+  const int32_t* trow = p.tables + (long)row * p.table_stride;
+
+  // Q^T operand: column c = member c/G, head c%G of this kv head's group.
+  const int cm = lr / G, cg = lr - (lr / G) * G;
+  uint4 qo[KS];
+  {
+    const int qidx = cm < nmem ? tld(item, 7 + (cm < kItemMembers ? cm : 0)) : -1;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      if (qidx >= 0 && lr < MG * G) {
+        const S* qp = (const S*)p.q + ((long)qidx * p.Hq + (long)head * G + cg) * D + 32 * s + 8 * lg;
+        qo[s] = *(const uint4*)qp;
+      } else {
+        qo[s] = make_uint4(0, 0, 0, 0);
+      }
+    }
+  }
+  const int k_lane = lr * D + 8 * lg;
+  const int v_lane = lr * B + 4 * lg;
+  float m = kNegInf, l = 0.f;
+  f32x4_t o[NT];
+#pragma unroll
+  for (int j = 0; j < NT; ++j) o[j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  auto load_tile = [&](int t, uint4 (&kr)[KS], uint2 (&vr)[NT], bool& okb) __attribute__((always_inline)) {
+    const int page = t / NSUB;
+    const int sub = t - page * NSUB;
+    int blk = -1;
+    if (t < t_last && page < p.table_stride) blk = tld(trow, page);
+    okb = blk >= 0 && blk < p.num_blocks;
+    const long ph = ((okb ? (long)blk : 0L) * p.Hkv + head) * (long)(B * D);
+    const int bytes = okb ? B * D * (int)sizeof(S) : 0;
+    const __amdgpu_buffer_rsrc_t rk = trsrc((const S*)p.k + ph, bytes);
+    const __amdgpu_buffer_rsrc_t rv = trsrc((const S*)p.v + ph, bytes);
+    const int ksub = sub * 16 * D * (int)sizeof(S);
+    const int vsub = sub * 16 * (int)sizeof(S);
+#pragma unroll
+    for (int s = 0; s < KS; ++s)
+      kr[s] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rk, (k_lane + 32 * s) * (int)sizeof(S), ksub, 0));
+#pragma unroll
+    for (int j = 0; j < NT; ++j)
+      vr[j] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rv, (v_lane + 16 * j * B) * (int)sizeof(S), vsub, 0));
+  };
+  auto compute_tile = [&](int t, bool okb, const uint4 (&kr)[KS], const uint2 (&vr)[NT]) __attribute__((always_inline)) {
+    f32x4_t st = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < KS; ++s) st = TMfma<T>::qk(kr[s], qo[s], st);
+    const int tok0 = t * 16 + 4 * lg;
+    float sc[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      sc[i] = st[i] * p.scale_log2;
+      if (!okb || tok0 + i >= valid) sc[i] = kNegInf;
+    }
+    float pm = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
+    pm = fmaxf(pm, __shfl_xor(pm, 16));
+    pm = fmaxf(pm, __shfl_xor(pm, 32));
+    const bool grow = (m == kNegInf) ? (pm != kNegInf) : (pm > m + kTreeSlack);
+    if (__builtin_amdgcn_ballot_w64(grow)) {
+      const float mn = fmaxf(m, pm);
+      const float alpha = (mn == kNegInf) ? 1.f : fast_exp2(m - mn);
+      l *= alpha;
+      m = mn;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float ar = __shfl(alpha, 4 * lg + i);
+#pragma unroll
+        for (int j = 0; j < NT; ++j) o[j][i] *= ar;
+      }
+    }
+    const float ms = (m == kNegInf) ? 0.f : m;
+    f32x4_t pr;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) pr[i] = fast_exp2(sc[i] - ms);
+    float ps = (pr[0] + pr[1]) + (pr[2] + pr[3]);
+    ps += __shfl_xor(ps, 16);
+    ps += __shfl_xor(ps, 32);
+    l += ps;
+    const uint2 pa = TMfma<T>::pack(pr);
+#pragma unroll
+    for (int j = 0; j < NT; ++j) o[j] = TMfma<T>::pv(pa, vr[j], o[j]);
+  };
+
+  uint4 k0[KS], k1[KS], k2[KS];
+  uint2 v0[NT], v1[NT], v2[NT];
+  bool ok0, ok1, ok2;
+  load_tile(t_first, k0, v0, ok0);
+  load_tile(t_first + 1, k1, v1, ok1);
+  for (int t = t_first; t < t_last; t += 3) {
+    load_tile(t + 2, k2, v2, ok2);
+    compute_tile(t, ok0, k0, v0);
+    if (t + 1 >= t_last) break;
+    load_tile(t + 3, k0, v0, ok0);
+    compute_tile(t + 1, ok1, k1, v1);
+    if (t + 2 >= t_last) break;
+    load_tile(t + 4, k1, v1, ok1);
+    compute_tile(t + 2, ok2, k2, v2);
+  }
+
+  // Partials: O row r = member r/G, head r%G (rows 4*lg + i); (m, l) per column lane.
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int r = 4 * lg + i;
+    const int mem = r / G, g = r - (r / G) * G;
+    if (r < MG * G && mem < nmem) {
+      float* wo = p.ws_o + ((long)(slot0 + mem) * G + g) * D + lr;
+#pragma unroll
+      for (int j = 0; j < NT; ++j) wo[16 * j] = o[j][i];
+    }
+  }
+  if (lane < 16 && cm < nmem && lane < MG * G) {
+    p.ws_ml[((long)(slot0 + cm) * G + cg) * 2] = m;
+    p.ws_ml[((long)(slot0 + cm) * G + cg) * 2 + 1] = l;
+  }
+}
+
+// Merge: one wavefront per (query, kv head); lane owns E = G*D/64 outputs.
+template <typename T, int D, int G>
+__global__ __launch_bounds__(64) void tree_merge_kernel(TreeParams p) {
+  constexpr int E = G * D / 64;
+  const int u = blockIdx.x;  // query * Hkv + head
+  if (u >= p.Nq * p.Hkv) return;
+  const int qi = u / p.Hkv, head = u - (u / p.Hkv) * p.Hkv;
+  const int lane = threadIdx.x;
+  const int g = (lane * E) / D, d0 = lane * E - g * D;
+  const int b = tld(p.q_slot_off, u), e = tld(p.q_slot_off, u + 1);
+  float M = kNegInf, L = 0.f, acc[E];
+#pragma unroll
+  for (int j = 0; j < E; ++j) acc[j] = 0.f;
+  for (int s = b; s < e; ++s) {
+    const long slot = tld(p.q_slots, s);
+    const float mp = p.ws_ml[(slot * G + g) * 2], lp = p.ws_ml[(slot * G + g) * 2 + 1];
+    const float* wo = p.ws_o + (slot * G + g) * D + d0;
+    const float mn = fmaxf(M, mp);
+    const float ms = (mn == kNegInf) ? 0.f : mn;
+    const float a = fast_exp2(M - ms), c = fast_exp2(mp - ms);
+    L = L * a + lp * c;
+#pragma unroll
+    for (int j = 0; j < E; ++j) acc[j] = acc[j] * a + wo[j] * c;
+    M = mn;
+  }
+  const float inv = L > 0.f ? 1.f / L : 0.f;
+  const long ob = ((long)qi * p.Hq + (long)head * G + g) * D + d0;
+#pragma unroll
+  for (int j = 0; j < E; ++j) Elem<T>::store1(p.out, ob + j, acc[j] * inv);
+}
+
+template <typename T, int D, int G, int B>
+static int tree_launch(const TreeParams& p, hipStream_t s) {
+  const int waves = kTreeThreads / 64;
+  if (p.n_items > 0)
+    hipLaunchKernelGGL((tree_decode_kernel<T, D, G, B>), dim3((p.n_items + waves - 1) / waves), dim3(kTreeThreads), 0,
+                       s, p);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return (int)e;
+  hipLaunchKernelGGL((tree_merge_kernel<T, D, G>), dim3(p.Nq * p.Hkv), dim3(64), 0, s, p);
+  return (int)hipGetLastError();
+}
+
+template <typename T, int D, int G>
+static int tree_b(const TreeParams& p, hipStream_t s) {
+  switch (p.B) {
+    case 16: return tree_launch<T, D, G, 16>(p, s);
+    case 32: return tree_launch<T, D, G, 32>(p, s);
+    case 64: return tree_launch<T, D, G, 64>(p, s);
+    default: return MENTAT_EUNSUP;
+  }
+}
+template <typename T, int D>
+static int tree_g(int G, const TreeParams& p, hipStream_t s) {
+  switch (G) {
+    case 1: return tree_b<T, D, 1>(p, s);
+    case 2: return tree_b<T, D, 2>(p, s);
+    case 4: return tree_b<T, D, 4>(p, s);
+    case 8: return tree_b<T, D, 8>(p, s);
+    case 16: return tree_b<T, D, 16>(p, s);
+    default: return MENTAT_EUNSUP;
+  }
+}
+template <typename T>
+static int tree_d(int D, int G, const TreeParams& p, hipStream_t s) {
+  switch (D) {
+    case 64: return tree_g<T, 64>(G, p, s);
+    case 128: return tree_g<T, 128>(G, p, s);
+    default: return MENTAT_EUNSUP;
+  }
+}
+
+}  // namespace mentat
+
+using namespace mentat;
+
+extern "C" size_t mentat_tree_decode_workspace_bytes(int n_slots, int Hq, int Hkv, int D) {
+  if (n_slots <= 0 || Hkv <= 0) return 0;
+  const int G = Hq / Hkv;
+  return (size_t)n_slots * G * (D + 2) * sizeof(float);
+}
+
+extern "C" int mentat_tree_decode(const void* q, const void* k_store, const void* v_store, const int32_t* block_tables,
+                                  int64_t table_stride, int64_t num_blocks, const int32_t* items, int n_items,
+                                  const int32_t* q_slot_offsets, const int32_t* q_slots, int n_slots, void* out,
+                                  int Nq, int Hq, int Hkv, int D, int block_size, float scale, int dtype,
+                                  void* workspace, size_t workspace_bytes, void* stream) {
+  if (Nq == 0) return MENTAT_OK;
+  if (!q || !k_store || !v_store || !block_tables || !out || !q_slot_offsets || Nq < 0 || Hq <= 0 || Hkv <= 0 ||
+      Hq % Hkv != 0 || table_stride <= 0 || num_blocks <= 0 || n_items < 0 || n_slots < 0)
+    return MENTAT_EINVAL;
+  if (n_items > 0 && (!items || !q_slots)) return MENTAT_EINVAL;
+  const size_t need = mentat_tree_decode_workspace_bytes(n_slots, Hq, Hkv, D);
+  if (need && (!workspace || workspace_bytes < need)) return MENTAT_ESPACE;
+  TreeParams p;
+  p.q = q; p.k = k_store; p.v = v_store; p.tables = block_tables; p.table_stride = table_stride;
+  p.num_blocks = num_blocks; p.items = items; p.n_items = n_items;
+  const int G = Hq / Hkv;
+  p.ws_o = (float*)workspace;
+  p.ws_ml = p.ws_o + (size_t)n_slots * G * D;
+  p.q_slot_off = q_slot_offsets; p.q_slots = q_slots; p.out = out;
+  p.Nq = Nq; p.Hq = Hq; p.Hkv = Hkv; p.B = block_size; p.scale_log2 = scale * kLog2e;
+  hipStream_t s = (hipStream_t)stream;
+  switch (dtype) {
+    case MENTAT_BF16: return tree_d<BF16>(D, G, p, s);
+    case MENTAT_F16: return tree_d<F16>(D, G, p, s);
+    default: return MENTAT_EUNSUP;
+  }
+}

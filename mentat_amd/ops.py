@@ -25,6 +25,7 @@ from ._lib import (
 
 __all__ = [
     "paged_decode",
+    "tree_decode",
     "kv_append",
     "page_copy",
     "table_copy_rows",
@@ -354,4 +355,66 @@ def philox4x32_10(counters: torch.Tensor, keys: torch.Tensor) -> torch.Tensor:
     out = torch.empty_like(c)
     st = get_lib().mentat_philox4x32_10(ptr(c), ptr(k), ptr(out), c.shape[0], stream_handle(dev))
     check(st, "mentat_philox4x32_10")
+    return out
+
+
+def tree_decode(
+    q: torch.Tensor,
+    k_store: torch.Tensor,
+    v_store: torch.Tensor,
+    *,
+    block_tables: torch.Tensor,
+    plan,
+    scale: Optional[float] = None,
+    out: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """Prefix-shared decode attention over native stores (mentat_tree_decode).
+
+    ``plan`` is a :class:`mentat_amd.tree_plan.TreePlan` built from the same
+    batch's page tables (one layer's ``block_tables`` [rows, stride] give the
+    page ids). Same result as :func:`paged_decode` on that batch.
+    """
+    _require(q.dim() == 3, f"q must be [N, Hq, D], got {tuple(q.shape)}")
+    Nq, Hq, D = q.shape
+    dev = q.device
+    _require(dev.type == "cuda", "tree_decode runs on the GPU only")
+    _require(q.dtype in (torch.bfloat16, torch.float16), "tree_decode needs a 16-bit dtype")
+    _require(k_store.dtype == q.dtype and v_store.dtype == q.dtype, "q/k/v dtypes differ")
+    _require(k_store.device == dev and v_store.device == dev, "q/k/v devices differ")
+    _require(q.is_contiguous() and k_store.is_contiguous() and v_store.is_contiguous(),
+             "q and the stores must be contiguous")
+    _require(k_store.dim() == 4, "native K store must be [num_blocks, Hkv, block_size, D]")
+    num_blocks, Hkv, block_size, Dk = k_store.shape
+    _require(tuple(v_store.shape) == (num_blocks, Hkv, Dk, block_size),
+             "native V store must be [num_blocks, Hkv, D, block_size]")
+    _require(Dk == D, f"head_dim mismatch q {D} vs cache {Dk}")
+    _require(Hq % Hkv == 0 and 16 % (Hq // Hkv) == 0, "Hq/Hkv must divide 16")
+    _require(block_size % 16 == 0, "tree_decode needs block_size % 16 == 0")
+    _require(block_tables.dim() == 2, "block_tables must be [rows, stride]")
+    _check_i32(block_tables, "block_tables", dev)
+    rows, _ = block_tables.shape
+    stride = block_tables.stride(0)
+    _require(block_tables.stride(1) == 1, "block_tables rows must be contiguous")
+    G = Hq // Hkv
+    if getattr(plan, "_validated", None) != (Nq, Hkv, G, rows, block_tables.shape[1], block_size):
+        plan.validate(Nq, Hkv, G, rows, block_tables.shape[1], block_size)
+        plan._validated = (Nq, Hkv, G, rows, block_tables.shape[1], block_size)
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    if out is None:
+        out = torch.empty_like(q)
+    else:
+        _require(out.shape == q.shape and out.dtype == q.dtype and out.is_contiguous(), "bad out")
+    if Nq == 0:
+        return out
+    items, off, slots = plan.device_arrays(dev)
+    lib = get_lib()
+    nbytes = lib.mentat_tree_decode_workspace_bytes(plan.n_slots, Hq, Hkv, D)
+    ws = workspace(dev, nbytes) if nbytes else None
+    st = lib.mentat_tree_decode(
+        ptr(q), ptr(k_store), ptr(v_store), ptr(block_tables), stride, num_blocks,
+        ptr(items), plan.items.shape[0], ptr(off), ptr(slots), plan.n_slots, ptr(out),
+        Nq, Hq, Hkv, D, block_size, float(scale), DTYPE_CODES[q.dtype], ptr(ws), nbytes, stream_handle(dev),
+    )
+    check(st, "mentat_tree_decode")
     return out

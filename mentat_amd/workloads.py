@@ -8,6 +8,12 @@ These are the measured workloads (sizes, distributions and seeds fixed here):
   context lengths uniform in [512, 4096], block tables = consecutive slices of
   a seeded random permutation of a 65,536-page pool, Q/K/V ~ N(0, 1),
   scale 1/sqrt(128).
+* ``prefix_tree_batch``: prefix-tree decode at Qwen3-8B attention shapes —
+  bf16, 32 query / 8 kv heads, head_dim 128, page size 16, q and k through
+  RMSNorm (weight 1, eps 1e-6), 4 trees of 32 leaves over 2048-token shared
+  prompts (``tree_ops`` fixes the shapes), written through the paged cache
+  manager so sharing, refcounts and copy-on-write are the manager's own.
+* ``sampling_logits``: [256, 151936] bf16 logits, row r ~ sigma_r * N(0, 1).
 """
 from __future__ import annotations
 
@@ -148,3 +154,174 @@ def sampling_logits(*, R: int = 256, V: int = 151936, sigma_lo: float = 0.5, sig
         z = torch.randn(r1 - r0, V, generator=g, device=device)
         x[r0:r1] = (z * torch.from_numpy(sig[r0:r1]).to(device)[:, None]).to(dtype)
     return x, sig
+
+
+# ----------------------------------------------------------------------------
+# Prefix-tree decode workload
+# ----------------------------------------------------------------------------
+
+def tree_ops(*, n_trees: int = 4, prefix: int = 2048, leaves: int = 32, max_private: int = 512,
+             seed: int = 0) -> list:
+    """Seeded event list that grows ``n_trees`` branching trees in a paged cache.
+
+    Shapes: each tree starts as one leaf with U{0..max_private} private tokens
+    after its ``prefix``-token prompt. A split picks a leaf uniformly and a
+    depth d uniformly along its private span [f, P] (f = depth of the leaf's
+    last fork, P = its length past the prompt); the leaf keeps P, a new leaf
+    starts at d with length U{d..max_private}; both leaves' private spans now
+    start at d. Splits repeat until the tree has ``leaves`` leaves.
+
+    The events replay that as decode would: one step appends one token to every
+    leaf still growing, forks happen at the step of their depth (in split
+    order), and a new leaf sits right after its parent in batch order, so the
+    parent (first in batch order) copies a shared partial tail on its next
+    append and the new leaf writes it in place.
+
+    Events: ("alloc", leaf), ("prefill", leaf, n), ("fork", parent, child),
+    ("step", [leaf, ...] in batch order). Leaves are numbered globally.
+    """
+    rng = np.random.default_rng(seed)
+    ops: list = []
+    forks_at: dict = {}
+    target: dict = {}
+    order: list = []
+    nid = 0
+    for _ in range(n_trees):
+        root = nid
+        nid += 1
+        f = {root: 0}
+        target[root] = int(rng.integers(0, max_private + 1))
+        live = [root]
+        while len(live) < leaves:
+            j = live[int(rng.integers(len(live)))]
+            d = int(rng.integers(f[j], target[j] + 1))
+            i = nid
+            nid += 1
+            target[i] = int(rng.integers(d, max_private + 1))
+            f[j] = f[i] = d
+            forks_at.setdefault(d, []).append((j, i))
+            live.append(i)
+        ops.append(("alloc", root))
+        ops.append(("prefill", root, prefix))
+        order.append(root)
+    for t in range(max_private + 1):
+        for j, i in forks_at.get(t, []):
+            ops.append(("fork", j, i))
+            order.insert(order.index(j) + 1, i)
+        grow = [x for x in order if target[x] > t]
+        if grow:
+            ops.append(("step", grow))
+    ops.append(("final", list(order)))
+    return ops
+
+
+def replay_tree_ops(mgr, ops: list, layer: int = 0, kv=None) -> tuple:
+    """Apply ``tree_ops`` events to a PagedKVCacheManager.
+
+    ``kv(n)`` returns the (k, v) rows [n, Hkv, D] to write; with ``kv=None``
+    only the host bookkeeping runs (page tables, refcounts, copy-on-write
+    decisions). Returns (sequence id of each leaf, leaves in batch order).
+    """
+    seq = {}
+    order = []
+    for op in ops:
+        if op[0] == "alloc":
+            seq[op[1]] = mgr.allocate_sequence()
+        elif op[0] == "prefill":
+            sid = seq[op[1]]
+            if kv is None:
+                mgr.plan_append(sid, layer, op[2])
+            else:
+                mgr.append_tokens(sid, layer, *kv(op[2]))
+        elif op[0] == "fork":
+            seq[op[2]] = mgr.fork_sequence(seq[op[1]])
+        elif op[0] == "step":
+            ids = [seq[x] for x in op[1]]
+            if kv is None:
+                mgr.plan_append_batched(ids, layer)
+            else:
+                mgr.append_tokens_batched(ids, layer, *kv(len(ids)))
+        elif op[0] == "final":
+            order = list(op[1])
+    return seq, order
+
+
+def _rms_normed(shape, g, device, eps=1e-6):
+    x = torch.randn(shape, generator=g, device=device, dtype=torch.float32)
+    return x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + eps)
+
+
+@dataclass
+class TreeBatch:
+    q: torch.Tensor            # [Nq, Hq, D], one query per leaf in batch order
+    mgr: object                # the PagedKVCacheManager holding the trees (one layer)
+    seq_ids: list              # sequence id of each query
+    lens: list                 # cached tokens of each query
+    tables: list               # host page table of each query
+    rows: list                 # device table row of each query
+    block_tables: torch.Tensor  # the layer's [rows, pages] int32 tables
+    seq_lens: torch.Tensor     # the layer's [rows] int32 lengths
+    k_store: torch.Tensor      # native stores of the layer
+    v_store: torch.Tensor
+    block_size: int
+    scale: float
+
+    def unique_tokens(self) -> int:
+        seen = set()
+        B = self.block_size
+        for t, n in zip(self.tables, self.lens):
+            for p in range((n + B - 1) // B):
+                seen.add((t[p], min(B, n - p * B)))
+        return sum(v for _, v in seen)
+
+    def logical_tokens(self) -> int:
+        return sum(self.lens)
+
+    def _bytes(self, tokens: int) -> int:
+        N, Hq, D = self.q.shape
+        Hkv = self.k_store.shape[1]
+        esz = self.q.element_size()
+        pages = sum((n + self.block_size - 1) // self.block_size for n in self.lens)
+        return tokens * Hkv * D * esz * 2 + 2 * N * Hq * D * esz + 4 * pages + 4 * N
+
+    def unique_bytes(self) -> int:
+        """K/V of every distinct cached token once, Q and O once, the table entries."""
+        return self._bytes(self.unique_tokens())
+
+    def logical_bytes(self) -> int:
+        """The same with every leaf's full context counted (no sharing)."""
+        return self._bytes(self.logical_tokens())
+
+
+def prefix_tree_batch(*, n_trees: int = 4, prefix: int = 2048, leaves: int = 32, max_private: int = 512,
+                      Hq: int = 32, Hkv: int = 8, D: int = 128, block_size: int = 16,
+                      max_blocks: int = 8192, dtype: torch.dtype = torch.bfloat16,
+                      device: str | torch.device = "cuda", seed: int = 0) -> TreeBatch:
+    from .core.paged_kv_cache import PagedKVCacheManager
+
+    ops = tree_ops(n_trees=n_trees, prefix=prefix, leaves=leaves, max_private=max_private, seed=seed)
+    mgr = PagedKVCacheManager(1, Hkv, D, max_blocks=max_blocks, block_size=block_size, device=device,
+                              dtype=dtype)
+    if mgr.layout != LAYOUT_NATIVE:
+        raise ValueError("the prefix-tree workload needs the native pool layout")
+    g = torch.Generator(device=device)
+    g.manual_seed(seed)
+
+    def kv(n):
+        k = _rms_normed((n, Hkv, D), g, device).to(dtype)
+        v = torch.randn(n, Hkv, D, generator=g, device=device).to(dtype)
+        return k, v
+
+    seq, order = replay_tree_ops(mgr, ops, 0, kv)
+    ids = [seq[x] for x in order]
+    q = _rms_normed((len(ids), Hq, D), g, device).to(dtype)
+    states = [mgr._sequences[s] for s in ids]
+    return TreeBatch(
+        q=q, mgr=mgr, seq_ids=ids,
+        lens=[st.num_tokens[0] for st in states],
+        tables=[list(st.page_table[0]) for st in states],
+        rows=[st.row for st in states],
+        block_tables=mgr._tables[0], seq_lens=mgr._lens[0],
+        k_store=mgr._k_store[0], v_store=mgr._v_store[0],
+        block_size=block_size, scale=1.0 / float(np.sqrt(D)),
+    )
