@@ -111,24 +111,29 @@ int mentat_paged_decode_auto_chunk(int N, int Hkv, int block_size, int max_seqle
  * bf16/f16, block_size 16/32/64, Hq/Hkv in {1,2,4,8,16}, D in {64,128}.
  *
  * The host plan (built once per decode step, shared by all layers):
- *   items[n_items][24] int32, one per (segment chunk, kv head, member group):
- *     [0] table row whose ids the chunk reads; [1] first 16-token tile;
- *     [2] tile count; [3] tokens of the segment (exclusive end, absolute);
- *     [4] kv head; [5] member count m (<= 16/(Hq/Hkv)); [6] first partial
- *     slot (member j writes slot [6]+j); [7..7+m) member query indices.
- *     Items with [2] == 0 are padding.
+ *   items[n_shared + n_solo][8] int32, one per (segment chunk, kv head,
+ *     member set): [0] table row whose ids the chunk reads; [1] first 16-token
+ *     tile; [2] tile count; [3] tokens of the segment (exclusive end,
+ *     absolute); [4] kv head; [5] member count m; [6] first partial slot
+ *     (member j writes slot [6]+j); [7] offset of the m member query indices
+ *     in members[]. Items with [2] == 0 are padding.
+ *     The first n_shared items are shared tasks (m <= 8 * 16/(Hq/Hkv)): one
+ *     workgroup stages the chunk's pages through LDS once for all members.
+ *     The other n_solo items have m <= 16/(Hq/Hkv) and run one per wavefront.
  *   q_slot_offsets[Nq*Hkv+1], q_slots[]: the partial slots of (query, kv head)
  *     q*Hkv+h, merged with the log-sum-exp rule into out.
  * block_tables: [rows, table_stride] int32 (one layer). Workspace:
  * mentat_tree_decode_workspace_bytes(n_slots, ...) bytes. Page ids outside
- * [0, num_blocks) are masked, not read.
+ * [0, num_blocks) are masked, not read. Every index the plan holds must be in
+ * range (rows, tiles, heads, members < Nq, slots < n_slots): the host
+ * validates plans before the call.
  * ---------------------------------------------------------------------- */
 size_t mentat_tree_decode_workspace_bytes(int n_slots, int Hq, int Hkv, int D);
 
 int mentat_tree_decode(const void* q, const void* k_store, const void* v_store, const int32_t* block_tables,
-                       int64_t table_stride, int64_t num_blocks, const int32_t* items, int n_items,
-                       const int32_t* q_slot_offsets, const int32_t* q_slots, int n_slots, void* out,
-                       int Nq, int Hq, int Hkv, int D, int block_size, float scale, int dtype,
+                       int64_t table_stride, int64_t num_blocks, const int32_t* items, int n_shared, int n_solo,
+                       const int32_t* members, const int32_t* q_slot_offsets, const int32_t* q_slots, int n_slots,
+                       void* out, int Nq, int Hq, int Hkv, int D, int block_size, float scale, int dtype,
                        void* workspace, size_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------------

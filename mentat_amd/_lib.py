@@ -57,8 +57,8 @@ SIGNATURES: dict[str, tuple] = {
         _c_int,
         [
             _c_void_p, _c_void_p, _c_void_p, _c_void_p,  # q, k_store, v_store, block_tables
-            _c_i64, _c_i64, _c_void_p, _c_int,  # table_stride, num_blocks, items, n_items
-            _c_void_p, _c_void_p, _c_int, _c_void_p,  # q_slot_offsets, q_slots, n_slots, out
+            _c_i64, _c_i64, _c_void_p, _c_int, _c_int,  # table_stride, num_blocks, items, n_shared, n_solo
+            _c_void_p, _c_void_p, _c_void_p, _c_int, _c_void_p,  # members, q_slot_offsets, q_slots, n_slots, out
             _c_int, _c_int, _c_int, _c_int, _c_int, _c_float, _c_int,  # Nq, Hq, Hkv, D, block_size, scale, dtype
             _c_void_p, _c_size, _c_void_p,  # workspace, workspace_bytes, stream
         ],

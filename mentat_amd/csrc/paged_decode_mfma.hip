@@ -244,11 +244,14 @@ __global__ __launch_bounds__(kNativeThreads) void paged_decode_mfma_kernel(Nativ
         sc[i] = st[i] * p.scale_log2;
         if (!okb || tok0 + i >= len) sc[i] = kNegInf;
       }
+      // m is uniform over the four lanes of a column; a lane compares its own
+      // four scores against it, and only when some lane has outgrown it by the
+      // slack is the column maximum formed (cross-lane) and the state rescaled.
       float pm = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
-      pm = fmaxf(pm, __shfl_xor(pm, 16));
-      pm = fmaxf(pm, __shfl_xor(pm, 32));
       const bool grow = (m == kNegInf) ? (pm != kNegInf) : (pm > m + kRescaleSlack);
       if (__builtin_amdgcn_ballot_w64(grow)) {
+        pm = fmaxf(pm, __shfl_xor(pm, 16));
+        pm = fmaxf(pm, __shfl_xor(pm, 32));
         const float mn = fmaxf(m, pm);
         const float alpha = (mn == kNegInf) ? 1.f : fast_exp2(m - mn);
         l *= alpha;
@@ -265,10 +268,7 @@ __global__ __launch_bounds__(kNativeThreads) void paged_decode_mfma_kernel(Nativ
       f32x4_t pr;
 #pragma unroll
       for (int i = 0; i < 4; ++i) pr[i] = fast_exp2(sc[i] - ms);
-      float ps = (pr[0] + pr[1]) + (pr[2] + pr[3]);
-      ps += __shfl_xor(ps, 16);
-      ps += __shfl_xor(ps, 32);
-      l += ps;
+      l += (pr[0] + pr[1]) + (pr[2] + pr[3]);  // per-lane partial sum, reduced after the loop
       const uint2 pa = Mfma<T>::pack(pr);
 #pragma unroll
       for (int j = 0; j < NT; ++j) o[j] = Mfma<T>::pv(pa, vr[j], o[j]);
@@ -292,6 +292,9 @@ __global__ __launch_bounds__(kNativeThreads) void paged_decode_mfma_kernel(Nativ
       load_tile(t + 4, k1, v1, ok1);
       compute_tile(t + 2, ok2, k2, v2);
     }
+
+    l += __shfl_xor(l, 16);
+    l += __shfl_xor(l, 32);
 
     // Emit: O rows (query heads) 4*lg + i, columns d = 16 j + lr.
     const bool whole = (f == ustart) && (seg_end == uend);

@@ -93,16 +93,6 @@ _Pragma("clang loop unroll(full)")
   }
 }
 
-// Compile-time loop: f(std::integral_constant<int, I>) for I = 0 .. N-1.
-template <typename F, int... I>
-__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
-  (f(std::integral_constant<int, I>{}), ...);
-}
-template <int N, typename F>
-__device__ __forceinline__ void static_for(F&& f) {
-  static_for_impl(f, std::make_integer_sequence<int, N>{});
-}
-
 // ---- element access ---------------------------------------------------------------------
 template <typename T> struct RowElem;
 template <> struct RowElem<BF16> {

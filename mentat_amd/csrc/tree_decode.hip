@@ -54,10 +54,14 @@ template <> struct TMfma<F16> {
 // Work item (int32 x kItemFields):
 //   [0] table row whose page ids the chunk reads   [1] first tile   [2] tile count
 //   [3] valid tokens: the chunk covers tokens [16*first, min(16*(first+count), valid))
-//   [4] kv head   [5] members (1 .. 16/G)   [6] first partial slot (member j -> slot + j)
-//   [7 ..] member query indices (kItemFields - 7 of them)
-constexpr int kItemFields = 24;
-constexpr int kItemMembers = kItemFields - 7;
+//   [4] kv head   [5] member count   [6] first partial slot (member j -> slot + j)
+//   [7] offset of the chunk's member query indices in `members`
+// Items [0, n_shared) are shared tasks, one workgroup each: the chunk's K/V tiles
+// are loaded once into LDS and each wavefront runs one group of 16/G members
+// (at most kTreeWaves groups). Items [n_shared, n_shared + n_solo) are solo
+// items, one per wavefront (at most 16/G members), reading K/V straight into
+// registers.
+constexpr int kItemFields = 8;
 
 struct TreeParams {
   const void* q;       // [Nq, Hq, D]
@@ -67,7 +71,8 @@ struct TreeParams {
   int64_t table_stride;
   int64_t num_blocks;
   const int32_t* items;
-  int n_items;
+  int n_shared, n_solo;
+  const int32_t* members;
   float* ws_o;         // [slots][G][D]
   float* ws_ml;        // [slots][G][2]
   // merge
@@ -78,7 +83,10 @@ struct TreeParams {
   float scale_log2;
 };
 
-constexpr int kTreeThreads = 512;  // 8 wavefronts
+constexpr int kTreeWaves = 8;
+constexpr int kTreeThreads = 64 * kTreeWaves;
+constexpr int kTreePrefetch = 8;        // shared path: tiles in flight per loading thread
+constexpr int kTreeSharedMaxTiles = 16;  // shared path: tiles per task (host-enforced)
 constexpr float kTreeSlack = 8.f;
 
 typedef const int32_t __attribute__((address_space(4)))* tconst_i32;
@@ -88,43 +96,220 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t trsrc(const void* base, int by
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes, 0x00020000);
 }
 
-template <typename T, int D, int G, int B>
-__global__ __launch_bounds__(kTreeThreads) void tree_decode_kernel(TreeParams p) {
-  constexpr int KS = D / 32, NT = D / 16, NSUB = B / 16, MG = 16 / G;
-  using S = typename T::storage;
-  const int lane = threadIdx.x & 63;
-  const int it = tuni(blockIdx.x * (kTreeThreads / 64) + (threadIdx.x >> 6));
-  if (it >= p.n_items) return;
-  const int32_t* item = p.items + (long)it * kItemFields;
-  const int row = tld(item, 0), t_first = tld(item, 1), ntile = tld(item, 2), valid = tld(item, 3);
-  const int head = tld(item, 4), nmem = tld(item, 5), slot0 = tld(item, 6);
-  if (ntile <= 0 || nmem <= 0) return;
-  const int t_last = t_first + ntile;
-  const int lr = lane & 15, lg = lane >> 4;
-  const int32_t* trow = p.tables + (long)row * p.table_stride;
+// LDS geometry of one staged 16-token tile (shared path). K rows are padded
+// by 16 bytes and V rows (16 tokens of one dim) by 8, which makes the MFMA
+// operand reads (16 lanes per row group) bank-conflict free.
+template <int D> struct TileLds {
+  static constexpr int KRS = 2 * D + 16;
+  static constexpr int VRS = 40;
+  static constexpr int KST = 16 * KRS;
+  static constexpr int STAGE = KST + D * VRS;
+};
 
-  // Q^T operand: column c = member c/G, head c%G of this kv head's group.
-  const int cm = lr / G, cg = lr - (lr / G) * G;
+// Online-softmax state of one wavefront: 16 query columns (member c/G, head
+// c%G), S^T = K.Q^T on v_mfma 16x16x32, O += P.V on 16x16x16.
+template <typename T, int D>
+struct WaveAttn {
+  static constexpr int KS = D / 32, NT = D / 16;
   uint4 qo[KS];
-  {
-    const int qidx = cm < nmem ? tld(item, 7 + (cm < kItemMembers ? cm : 0)) : -1;
+  f32x4_t o[NT];
+  float m, l;
+  int lr, lg;
+
+  __device__ __forceinline__ void init(const TreeParams& p, int lane, int qidx, int head, int G) {
+    using S = typename T::storage;
+    lr = lane & 15;
+    lg = lane >> 4;
+    const int cg = lr % G;
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
-      if (qidx >= 0 && lr < MG * G) {
+      if (qidx >= 0) {
         const S* qp = (const S*)p.q + ((long)qidx * p.Hq + (long)head * G + cg) * D + 32 * s + 8 * lg;
         qo[s] = *(const uint4*)qp;
       } else {
         qo[s] = make_uint4(0, 0, 0, 0);
       }
     }
-  }
-  const int k_lane = lr * D + 8 * lg;
-  const int v_lane = lr * B + 4 * lg;
-  float m = kNegInf, l = 0.f;
-  f32x4_t o[NT];
+    m = kNegInf;
+    l = 0.f;
 #pragma unroll
-  for (int j = 0; j < NT; ++j) o[j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < NT; ++j) o[j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  }
 
+  // kr[s]: K rows (token lr, dims 32s + 8lg ..+7); vr[j]: V (dim lr + 16j, tokens 4lg ..+3).
+  __device__ __forceinline__ void tile(const TreeParams& p, int t, bool okb, int valid, const uint4 (&kr)[KS],
+                                       const uint2 (&vr)[NT]) {
+    f32x4_t st = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < KS; ++s) st = TMfma<T>::qk(kr[s], qo[s], st);
+    const int tok0 = t * 16 + 4 * lg;
+    float sc[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      sc[i] = st[i] * p.scale_log2;
+      if (!okb || tok0 + i >= valid) sc[i] = kNegInf;
+    }
+    // m is uniform over the four lanes of a column; a lane compares its own
+    // four scores against it, and only when some lane has outgrown it by the
+    // slack is the column maximum formed (cross-lane) and the state rescaled.
+    float pm = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
+    const bool grow = (m == kNegInf) ? (pm != kNegInf) : (pm > m + kTreeSlack);
+    if (__builtin_amdgcn_ballot_w64(grow)) {
+      pm = fmaxf(pm, __shfl_xor(pm, 16));
+      pm = fmaxf(pm, __shfl_xor(pm, 32));
+      const float mn = fmaxf(m, pm);
+      const float alpha = (mn == kNegInf) ? 1.f : fast_exp2(m - mn);
+      l *= alpha;
+      m = mn;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float ar = __shfl(alpha, 4 * lg + i);
+#pragma unroll
+        for (int j = 0; j < NT; ++j) o[j][i] *= ar;
+      }
+    }
+    const float ms = (m == kNegInf) ? 0.f : m;
+    f32x4_t pr;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) pr[i] = fast_exp2(sc[i] - ms);
+    l += (pr[0] + pr[1]) + (pr[2] + pr[3]);  // per-lane partial sum, reduced in emit()
+    const uint2 pa = TMfma<T>::pack(pr);
+#pragma unroll
+    for (int j = 0; j < NT; ++j) o[j] = TMfma<T>::pv(pa, vr[j], o[j]);
+  }
+
+  // Partials of members [0, nmem) of this wave's group; member j -> slot slot0 + j.
+  __device__ __forceinline__ void emit(const TreeParams& p, int nmem, int slot0, int G) {
+    l += __shfl_xor(l, 16);
+    l += __shfl_xor(l, 32);
+    const int mg = 16 / G;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = 4 * lg + i;  // O row = query column r: member r/G, head r%G
+      const int mem = r / G, g = r % G;
+      if (mem < nmem && mem < mg) {
+        float* wo = p.ws_o + ((long)(slot0 + mem) * G + g) * D + lr;
+#pragma unroll
+        for (int j = 0; j < NT; ++j) wo[16 * j] = o[j][i];
+      }
+    }
+    if (lg == 0 && lr / G < nmem) {
+      float* ml = p.ws_ml + ((long)(slot0 + lr / G) * G + lr % G) * 2;
+      ml[0] = m;
+      ml[1] = l;
+    }
+  }
+};
+
+// Shared task: the workgroup streams the chunk's tiles through a two-stage LDS
+// ring (every loading thread keeps kTreePrefetch 16-byte loads in flight), one
+// barrier per tile; wave w computes member group w.
+template <typename T, int D, int G, int B>
+__device__ __forceinline__ void tree_shared(const TreeParams& p, const int32_t* item, char* lds) {
+  using L = TileLds<D>;
+  using S = typename T::storage;
+  constexpr int KS = D / 32, NT = D / 16, NSUB = B / 16, MG = 16 / G;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = tuni(tid >> 6);
+  const int row = tld(item, 0), t_first = tld(item, 1), ntile = tld(item, 2), valid = tld(item, 3);
+  const int head = tld(item, 4), nmem = tld(item, 5), slot0 = tld(item, 6), moff = tld(item, 7);
+  if (ntile <= 0 || ntile > kTreeSharedMaxTiles || nmem <= 0) return;  // uniform over the workgroup
+  const int t_last = t_first + ntile;
+  const int32_t* trow = p.tables + (long)row * p.table_stride;
+
+  // This thread's 16-byte piece of every tile: waves [0, 2D/64) carry K,
+  // waves [2D/64, 4D/64) carry V, the rest carry nothing (D = 64).
+  const bool loader = wave * 64 < 4 * D;
+  const bool is_k = wave * 64 < 2 * D;
+  int goff, loff;
+  if (is_k) {
+    const int tok = tid / (D / 8), dc = tid % (D / 8);
+    goff = (tok * D + dc * 8) * (int)sizeof(S);
+    loff = tok * L::KRS + dc * 16;
+  } else {
+    const int c = loader ? tid - 2 * D : 0;
+    const int d = c >> 1, h = c & 1;
+    goff = (d * B + h * 8) * (int)sizeof(S);
+    loff = L::KST + d * L::VRS + h * 16;
+  }
+  const S* base = (const S*)(is_k ? p.k : p.v);
+  auto issue = [&](int t) __attribute__((always_inline)) -> uint4 {
+    const int page = t / NSUB, sub = t - page * NSUB;
+    int blk = -1;
+    if (t < t_last && page < p.table_stride) blk = tld(trow, page);
+    const bool okb = blk >= 0 && blk < p.num_blocks && loader;
+    const long ph = ((okb ? (long)blk : 0L) * p.Hkv + head) * (long)(B * D);
+    const __amdgpu_buffer_rsrc_t r = trsrc(base + ph, okb ? B * D * (int)sizeof(S) : 0);
+    const int soff = (is_k ? sub * 16 * D : sub * 16) * (int)sizeof(S);
+    return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, goff, soff, 0));
+  };
+
+  // The tile loop is fully unrolled (ntile <= kTreeSharedMaxTiles): with no
+  // back edge, every wait for a prefetched tile counts exactly the loads
+  // issued after it.
+  uint4 pf[kTreePrefetch];
+  static_for<kTreePrefetch>([&](auto ic) __attribute__((always_inline)) {
+    constexpr int i = decltype(ic)::value;
+    pf[i] = issue(t_first + i);
+  });
+  // The query loads (member index, then q) go out after the first tiles.
+  const int g0 = wave * MG;
+  const bool active = g0 < nmem;
+  WaveAttn<T, D> w;
+  {
+    const int cm = (lane & 15) / G;
+    const int qidx = (active && g0 + cm < nmem) ? p.members[moff + g0 + cm] : -1;
+    w.init(p, lane, qidx, head, G);
+  }
+  static_for<kTreeSharedMaxTiles>([&](auto ic) __attribute__((always_inline)) {
+    constexpr int i = decltype(ic)::value;
+    if (i < ntile) {
+      const int t = t_first + i;
+      char* stg = lds + (i & 1) * L::STAGE;
+      const uint4 cur = pf[i % kTreePrefetch];
+      if (loader) {
+        if (is_k) {
+          *(uint4*)__builtin_assume_aligned(stg + loff, 16) = cur;
+        } else {
+          *(uint2*)__builtin_assume_aligned(stg + loff, 8) = make_uint2(cur.x, cur.y);
+          *(uint2*)__builtin_assume_aligned(stg + loff + 8, 8) = make_uint2(cur.z, cur.w);
+        }
+      }
+      if constexpr (i + kTreePrefetch < kTreeSharedMaxTiles) pf[i % kTreePrefetch] = issue(t + kTreePrefetch);
+      __syncthreads();
+      if (active) {
+        const int page = t / NSUB;
+        const int blk = page < p.table_stride ? tld(trow, page) : -1;
+        const bool okb = blk >= 0 && blk < p.num_blocks;
+        uint4 kr[KS];
+        uint2 vr[NT];
+#pragma unroll
+        for (int s = 0; s < KS; ++s)
+          kr[s] = *(const uint4*)__builtin_assume_aligned(stg + w.lr * L::KRS + (4 * s + w.lg) * 16, 16);
+#pragma unroll
+        for (int j = 0; j < NT; ++j)
+          vr[j] = *(const uint2*)__builtin_assume_aligned(stg + L::KST + (w.lr + 16 * j) * L::VRS + w.lg * 8, 8);
+        w.tile(p, t, okb, valid, kr, vr);
+      }
+    }
+  });
+  if (active) w.emit(p, nmem - g0, slot0 + g0, G);
+}
+
+// Solo item: one wavefront, K/V straight into a three-tile register ring.
+template <typename T, int D, int G, int B>
+__device__ __forceinline__ void tree_solo(const TreeParams& p, const int32_t* item) {
+  using S = typename T::storage;
+  constexpr int KS = D / 32, NT = D / 16, NSUB = B / 16;
+  const int lane = threadIdx.x & 63;
+  const int row = tld(item, 0), t_first = tld(item, 1), ntile = tld(item, 2), valid = tld(item, 3);
+  const int head = tld(item, 4), nmem = tld(item, 5), slot0 = tld(item, 6), moff = tld(item, 7);
+  if (ntile <= 0 || nmem <= 0) return;
+  const int t_last = t_first + ntile;
+  const int32_t* trow = p.tables + (long)row * p.table_stride;
+  WaveAttn<T, D> w;
+  const int k_lane = (lane & 15) * D + 8 * (lane >> 4);
+  const int v_lane = (lane & 15) * B + 4 * (lane >> 4);
   auto load_tile = [&](int t, uint4 (&kr)[KS], uint2 (&vr)[NT], bool& okb) __attribute__((always_inline)) {
     const int page = t / NSUB;
     const int sub = t - page * NSUB;
@@ -144,105 +329,88 @@ __global__ __launch_bounds__(kTreeThreads) void tree_decode_kernel(TreeParams p)
     for (int j = 0; j < NT; ++j)
       vr[j] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rv, (v_lane + 16 * j * B) * (int)sizeof(S), vsub, 0));
   };
-  auto compute_tile = [&](int t, bool okb, const uint4 (&kr)[KS], const uint2 (&vr)[NT]) __attribute__((always_inline)) {
-    f32x4_t st = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int s = 0; s < KS; ++s) st = TMfma<T>::qk(kr[s], qo[s], st);
-    const int tok0 = t * 16 + 4 * lg;
-    float sc[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      sc[i] = st[i] * p.scale_log2;
-      if (!okb || tok0 + i >= valid) sc[i] = kNegInf;
-    }
-    float pm = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
-    pm = fmaxf(pm, __shfl_xor(pm, 16));
-    pm = fmaxf(pm, __shfl_xor(pm, 32));
-    const bool grow = (m == kNegInf) ? (pm != kNegInf) : (pm > m + kTreeSlack);
-    if (__builtin_amdgcn_ballot_w64(grow)) {
-      const float mn = fmaxf(m, pm);
-      const float alpha = (mn == kNegInf) ? 1.f : fast_exp2(m - mn);
-      l *= alpha;
-      m = mn;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float ar = __shfl(alpha, 4 * lg + i);
-#pragma unroll
-        for (int j = 0; j < NT; ++j) o[j][i] *= ar;
-      }
-    }
-    const float ms = (m == kNegInf) ? 0.f : m;
-    f32x4_t pr;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) pr[i] = fast_exp2(sc[i] - ms);
-    float ps = (pr[0] + pr[1]) + (pr[2] + pr[3]);
-    ps += __shfl_xor(ps, 16);
-    ps += __shfl_xor(ps, 32);
-    l += ps;
-    const uint2 pa = TMfma<T>::pack(pr);
-#pragma unroll
-    for (int j = 0; j < NT; ++j) o[j] = TMfma<T>::pv(pa, vr[j], o[j]);
-  };
-
   uint4 k0[KS], k1[KS], k2[KS];
   uint2 v0[NT], v1[NT], v2[NT];
   bool ok0, ok1, ok2;
   load_tile(t_first, k0, v0, ok0);
   load_tile(t_first + 1, k1, v1, ok1);
+  {  // the query loads (member index, then q) go out after the first tiles
+    const int cm = (lane & 15) / G;
+    w.init(p, lane, cm < nmem ? p.members[moff + cm] : -1, head, G);
+  }
   for (int t = t_first; t < t_last; t += 3) {
     load_tile(t + 2, k2, v2, ok2);
-    compute_tile(t, ok0, k0, v0);
+    w.tile(p, t, ok0, valid, k0, v0);
     if (t + 1 >= t_last) break;
     load_tile(t + 3, k0, v0, ok0);
-    compute_tile(t + 1, ok1, k1, v1);
+    w.tile(p, t + 1, ok1, valid, k1, v1);
     if (t + 2 >= t_last) break;
     load_tile(t + 4, k1, v1, ok1);
-    compute_tile(t + 2, ok2, k2, v2);
+    w.tile(p, t + 2, ok2, valid, k2, v2);
   }
-
-  // Partials: O row r = member r/G, head r%G (rows 4*lg + i); (m, l) per column lane.
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int r = 4 * lg + i;
-    const int mem = r / G, g = r - (r / G) * G;
-    if (r < MG * G && mem < nmem) {
-      float* wo = p.ws_o + ((long)(slot0 + mem) * G + g) * D + lr;
-#pragma unroll
-      for (int j = 0; j < NT; ++j) wo[16 * j] = o[j][i];
-    }
-  }
-  if (lane < 16 && cm < nmem && lane < MG * G) {
-    p.ws_ml[((long)(slot0 + cm) * G + cg) * 2] = m;
-    p.ws_ml[((long)(slot0 + cm) * G + cg) * 2 + 1] = l;
-  }
+  w.emit(p, nmem, slot0, G);
 }
 
-// Merge: one wavefront per (query, kv head); lane owns E = G*D/64 outputs.
+template <typename T, int D, int G, int B>
+__global__ __launch_bounds__(kTreeThreads) void tree_decode_kernel(TreeParams p) {
+  __shared__ uint4 lds_words[2 * TileLds<D>::STAGE / 16];
+  char* lds = (char*)lds_words;
+  const int bid = blockIdx.x;
+  if (bid < p.n_shared) {
+    tree_shared<T, D, G, B>(p, p.items + (long)bid * kItemFields, lds);
+    return;
+  }
+  const int it = p.n_shared + (bid - p.n_shared) * kTreeWaves + tuni(threadIdx.x >> 6);
+  if (it >= p.n_shared + p.n_solo) return;
+  tree_solo<T, D, G, B>(p, p.items + (long)it * kItemFields);
+}
+
+// Merge: one wavefront per (query, kv head). The column maxima M_g and sums
+// L_g come from a pass over the (slot, head) pairs spread across the lanes
+// (lane j always has head j % G); the output pass then weights every slot's
+// partial O by exp2(m - M_g), loads that do not depend on one another.
 template <typename T, int D, int G>
 __global__ __launch_bounds__(64) void tree_merge_kernel(TreeParams p) {
-  constexpr int E = G * D / 64;
-  const int u = blockIdx.x;  // query * Hkv + head
+  constexpr int E = G * D / 64;  // outputs per lane
+  const int u = blockIdx.x;      // query * Hkv + head
   if (u >= p.Nq * p.Hkv) return;
   const int qi = u / p.Hkv, head = u - (u / p.Hkv) * p.Hkv;
   const int lane = threadIdx.x;
-  const int g = (lane * E) / D, d0 = lane * E - g * D;
   const int b = tld(p.q_slot_off, u), e = tld(p.q_slot_off, u + 1);
-  float M = kNegInf, L = 0.f, acc[E];
+  const int n = e - b;
+  // pass 1: per-lane max over its (slot, head lane % G) pairs, then over lanes of one head
+  const int gl = lane % G;
+  float mx = kNegInf;
+  for (int i = lane; i < n * G; i += 64) {
+    const long slot = p.q_slots[b + i / G];
+    mx = fmaxf(mx, p.ws_ml[(slot * G + gl) * 2]);
+  }
+#pragma unroll
+  for (int off = G; off < 64; off <<= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+  const float mref = (mx == kNegInf) ? 0.f : mx;
+  float ls = 0.f;
+  for (int i = lane; i < n * G; i += 64) {
+    const long slot = p.q_slots[b + i / G];
+    const float* ml = p.ws_ml + (slot * G + gl) * 2;
+    ls += ml[1] * fast_exp2(ml[0] - mref);
+  }
+#pragma unroll
+  for (int off = G; off < 64; off <<= 1) ls += __shfl_xor(ls, off);
+  // pass 2: this lane's E outputs of head g
+  const int g = (lane * E) / D, d0 = lane * E - g * D;
+  const float Mg = __shfl(mref, g), Lg = __shfl(ls, g);
+  float acc[E];
 #pragma unroll
   for (int j = 0; j < E; ++j) acc[j] = 0.f;
+#pragma unroll 4
   for (int s = b; s < e; ++s) {
     const long slot = tld(p.q_slots, s);
-    const float mp = p.ws_ml[(slot * G + g) * 2], lp = p.ws_ml[(slot * G + g) * 2 + 1];
+    const float c = fast_exp2(p.ws_ml[(slot * G + g) * 2] - Mg);
     const float* wo = p.ws_o + (slot * G + g) * D + d0;
-    const float mn = fmaxf(M, mp);
-    const float ms = (mn == kNegInf) ? 0.f : mn;
-    const float a = fast_exp2(M - ms), c = fast_exp2(mp - ms);
-    L = L * a + lp * c;
 #pragma unroll
-    for (int j = 0; j < E; ++j) acc[j] = acc[j] * a + wo[j] * c;
-    M = mn;
+    for (int j = 0; j < E; ++j) acc[j] += wo[j] * c;
   }
-  const float inv = L > 0.f ? 1.f / L : 0.f;
+  const float inv = Lg > 0.f ? 1.f / Lg : 0.f;
   const long ob = ((long)qi * p.Hq + (long)head * G + g) * D + d0;
 #pragma unroll
   for (int j = 0; j < E; ++j) Elem<T>::store1(p.out, ob + j, acc[j] * inv);
@@ -250,10 +418,9 @@ __global__ __launch_bounds__(64) void tree_merge_kernel(TreeParams p) {
 
 template <typename T, int D, int G, int B>
 static int tree_launch(const TreeParams& p, hipStream_t s) {
-  const int waves = kTreeThreads / 64;
-  if (p.n_items > 0)
-    hipLaunchKernelGGL((tree_decode_kernel<T, D, G, B>), dim3((p.n_items + waves - 1) / waves), dim3(kTreeThreads), 0,
-                       s, p);
+  const int blocks = p.n_shared + (p.n_solo + kTreeWaves - 1) / kTreeWaves;
+  if (blocks > 0)
+    hipLaunchKernelGGL((tree_decode_kernel<T, D, G, B>), dim3(blocks), dim3(kTreeThreads), 0, s, p);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return (int)e;
   hipLaunchKernelGGL((tree_merge_kernel<T, D, G>), dim3(p.Nq * p.Hkv), dim3(64), 0, s, p);
@@ -300,20 +467,21 @@ extern "C" size_t mentat_tree_decode_workspace_bytes(int n_slots, int Hq, int Hk
 }
 
 extern "C" int mentat_tree_decode(const void* q, const void* k_store, const void* v_store, const int32_t* block_tables,
-                                  int64_t table_stride, int64_t num_blocks, const int32_t* items, int n_items,
-                                  const int32_t* q_slot_offsets, const int32_t* q_slots, int n_slots, void* out,
-                                  int Nq, int Hq, int Hkv, int D, int block_size, float scale, int dtype,
-                                  void* workspace, size_t workspace_bytes, void* stream) {
+                                  int64_t table_stride, int64_t num_blocks, const int32_t* items, int n_shared,
+                                  int n_solo, const int32_t* members, const int32_t* q_slot_offsets,
+                                  const int32_t* q_slots, int n_slots, void* out, int Nq, int Hq, int Hkv, int D,
+                                  int block_size, float scale, int dtype, void* workspace, size_t workspace_bytes,
+                                  void* stream) {
   if (Nq == 0) return MENTAT_OK;
   if (!q || !k_store || !v_store || !block_tables || !out || !q_slot_offsets || Nq < 0 || Hq <= 0 || Hkv <= 0 ||
-      Hq % Hkv != 0 || table_stride <= 0 || num_blocks <= 0 || n_items < 0 || n_slots < 0)
+      Hq % Hkv != 0 || table_stride <= 0 || num_blocks <= 0 || n_shared < 0 || n_solo < 0 || n_slots < 0)
     return MENTAT_EINVAL;
-  if (n_items > 0 && (!items || !q_slots)) return MENTAT_EINVAL;
+  if (n_shared + n_solo > 0 && (!items || !members || !q_slots)) return MENTAT_EINVAL;
   const size_t need = mentat_tree_decode_workspace_bytes(n_slots, Hq, Hkv, D);
   if (need && (!workspace || workspace_bytes < need)) return MENTAT_ESPACE;
   TreeParams p;
   p.q = q; p.k = k_store; p.v = v_store; p.tables = block_tables; p.table_stride = table_stride;
-  p.num_blocks = num_blocks; p.items = items; p.n_items = n_items;
+  p.num_blocks = num_blocks; p.items = items; p.n_shared = n_shared; p.n_solo = n_solo; p.members = members;
   const int G = Hq / Hkv;
   p.ws_o = (float*)workspace;
   p.ws_ml = p.ws_o + (size_t)n_slots * G * D;

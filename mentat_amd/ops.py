@@ -407,13 +407,13 @@ def tree_decode(
         _require(out.shape == q.shape and out.dtype == q.dtype and out.is_contiguous(), "bad out")
     if Nq == 0:
         return out
-    items, off, slots = plan.device_arrays(dev)
+    items, members, off, slots = plan.device_arrays(dev)
     lib = get_lib()
     nbytes = lib.mentat_tree_decode_workspace_bytes(plan.n_slots, Hq, Hkv, D)
     ws = workspace(dev, nbytes) if nbytes else None
     st = lib.mentat_tree_decode(
         ptr(q), ptr(k_store), ptr(v_store), ptr(block_tables), stride, num_blocks,
-        ptr(items), plan.items.shape[0], ptr(off), ptr(slots), plan.n_slots, ptr(out),
+        ptr(items), plan.n_shared, plan.n_solo, ptr(members), ptr(off), ptr(slots), plan.n_slots, ptr(out),
         Nq, Hq, Hkv, D, block_size, float(scale), DTYPE_CODES[q.dtype], ptr(ws), nbytes, stream_handle(dev),
     )
     check(st, "mentat_tree_decode")

@@ -35,10 +35,10 @@ def _oracle(tb, idx=None):
     return paged_decode_f64(q, kc, vc, tabs, [tb.lens[i] for i in idx], tb.block_size, tb.scale)
 
 
-def _run_tree(tb, chunk_tiles=16):
+def _run_tree(tb, chunk_tiles=16, min_groups=3):
     G = tb.q.shape[1] // tb.k_store.shape[1]
     plan = build_plan(tb.tables, tb.lens, tb.rows, block_size=tb.block_size, Hkv=tb.k_store.shape[1], G=G,
-                      chunk_tiles=chunk_tiles)
+                      chunk_tiles=chunk_tiles, shared_chunk_tiles=min(16, chunk_tiles + 1), shared_min_groups=min_groups)
     out = ops.tree_decode(tb.q, tb.k_store, tb.v_store, block_tables=tb.block_tables, plan=plan, scale=tb.scale)
     torch.cuda.synchronize()
     return out, plan
@@ -51,11 +51,13 @@ def _close(got, want, what):
     assert err.max() <= 0, (what, float(np.abs(got - want).max()))
 
 
-def test_tree_decode_qwen3_8b_trees(gpu):
-    """4 trees x 32 leaves over 2048-token prompts, Qwen3-8B attention shapes."""
-    print("case tree qwen3-8b full", flush=True)
+@pytest.mark.parametrize("min_groups", [3, 1, 99])
+def test_tree_decode_qwen3_8b_trees(gpu, min_groups):
+    """4 trees x 32 leaves over 2048-token prompts, Qwen3-8B attention shapes; shared
+    tasks for chunks of >= min_groups member groups (1: all, 99: none)."""
+    print(f"case tree qwen3-8b full min_groups={min_groups}", flush=True)
     tb = prefix_tree_batch(device="cuda", seed=0)
-    out, plan = _run_tree(tb)
+    out, plan = _run_tree(tb, min_groups=min_groups)
     assert plan.unique_tokens() < 0.1 * tb.logical_tokens()
     rows_t = torch.tensor(tb.rows, dtype=torch.int32, device="cuda")
     ref = ops.paged_decode(tb.q, tb.k_store, tb.v_store, max_seqlen=max(tb.lens), block_tables=tb.block_tables,
@@ -76,11 +78,13 @@ def test_tree_decode_qwen3_8b_trees(gpu):
     (32, 2, 64, 16, torch.float16, 64),
 ])
 def test_tree_decode_shapes(gpu, Hq, Hkv, D, B, dtype, chunk):
-    print(f"case tree Hq={Hq} Hkv={Hkv} D={D} B={B} {dtype} chunk={chunk}", flush=True)
     tb = prefix_tree_batch(n_trees=2, prefix=150, leaves=9, max_private=70, Hq=Hq, Hkv=Hkv, D=D, block_size=B,
                            max_blocks=512, dtype=dtype, device="cuda", seed=Hq + D + B)
-    out, _ = _run_tree(tb, chunk_tiles=chunk)
-    _close(out.float().cpu().numpy(), _oracle(tb), "tree vs oracle")
+    want = _oracle(tb)
+    for min_groups in (1, 2, 99):
+        print(f"case tree Hq={Hq} Hkv={Hkv} D={D} B={B} {dtype} chunk={chunk} min_groups={min_groups}", flush=True)
+        out, _ = _run_tree(tb, chunk_tiles=chunk, min_groups=min_groups)
+        _close(out.float().cpu().numpy(), want, ("tree vs oracle", min_groups))
 
 
 def test_tree_decode_no_sharing_and_tiny(gpu):
@@ -89,14 +93,16 @@ def test_tree_decode_no_sharing_and_tiny(gpu):
     for prefix, leaves, priv in ((1, 3, 5), (7, 4, 0), (16, 2, 1)):
         tb = prefix_tree_batch(n_trees=3, prefix=prefix, leaves=leaves, max_private=priv, Hq=8, Hkv=2, D=64,
                                max_blocks=256, device="cuda", seed=prefix)
-        out, _ = _run_tree(tb, chunk_tiles=1)
-        _close(out.float().cpu().numpy(), _oracle(tb), ("tiny", prefix, leaves, priv))
+        want = _oracle(tb)
+        for min_groups in (1, 99):
+            out, _ = _run_tree(tb, chunk_tiles=1, min_groups=min_groups)
+            _close(out.float().cpu().numpy(), want, ("tiny", prefix, leaves, priv, min_groups))
 
 
 def test_tree_decode_rejects_bad_plans(gpu):
     tb = prefix_tree_batch(n_trees=1, prefix=40, leaves=3, max_private=8, Hq=8, Hkv=2, D=64, max_blocks=128,
                            device="cuda", seed=1)
     plan = build_plan(tb.tables, tb.lens, tb.rows, block_size=16, Hkv=2, G=4)
-    plan.items[0, 7] = len(tb.seq_ids)  # member index past the batch
+    plan.members[0] = len(tb.seq_ids)  # member index past the batch
     with pytest.raises(ValueError):
         ops.tree_decode(tb.q, tb.k_store, tb.v_store, block_tables=tb.block_tables, plan=plan)

@@ -12,7 +12,7 @@ import pytest
 import torch
 
 from mentat_amd.core.paged_kv_cache import PagedKVCacheManager
-from mentat_amd.tree_plan import ITEM_FIELDS, ITEM_MEMBERS, WAVES_PER_WG, build_plan, find_segments
+from mentat_amd.tree_plan import ITEM_FIELDS, WAVES_PER_WG, build_plan, find_segments
 from mentat_amd.workloads import replay_tree_ops, tree_ops
 from oracle.attention import paged_decode_f64
 from oracle.paged_cache import OracleCache
@@ -104,27 +104,33 @@ def test_segments_partition_each_context(seed):
     assert uniq < 0.5 * sum(lens)  # the 2048-token prompts dominate
 
 
-def test_plan_items_and_slots():
+@pytest.mark.parametrize("min_groups", [1, 3, 99])
+def test_plan_items_and_slots(min_groups):
     m, _, ids, tables, lens, rows = _host_trees(0)
     Hkv, G = 8, 4
-    plan = build_plan(tables, lens, rows, block_size=16, Hkv=Hkv, G=G, chunk_tiles=16)
+    mg = 16 // G
+    plan = build_plan(tables, lens, rows, block_size=16, Hkv=Hkv, G=G, chunk_tiles=16,
+                      shared_min_groups=min_groups)
     plan.validate(len(ids), Hkv, G, max(rows) + 1, max(len(t) for t in tables), 16)
     it = plan.items
     assert it.shape[1] == ITEM_FIELDS and it.dtype == np.int32
-    live = it[it[:, 2] > 0]
-    assert live[:, 5].max() <= min(16 // G, ITEM_MEMBERS)
+    sh, so = it[: plan.n_shared], it[plan.n_shared:]
+    assert (so[:, 5] <= mg).all() and (sh[:, 5] <= WAVES_PER_WG * mg).all()
+    if min_groups == 99:
+        assert plan.n_shared == 0
+    else:
+        assert plan.n_shared > 0 and (sh[:, 5] > (min_groups - 1) * mg).all()
     # each slot written exactly once and listed exactly once
-    written = np.concatenate([np.arange(a[6], a[6] + a[5]) for a in live])
+    written = np.concatenate([np.arange(a[6], a[6] + a[5]) for a in it])
     assert sorted(written.tolist()) == list(range(plan.n_slots))
     assert sorted(plan.q_slots[: plan.q_slot_offsets[-1]].tolist()) == list(range(plan.n_slots))
-    # groups of one shared (chunk, head) never straddle a workgroup when they fit in one
-    pos = {}
-    for idx, a in enumerate(it):
-        if a[2] > 0:
-            pos.setdefault((a[0], a[1], a[4]), []).append(idx)
-    for key, idxs in pos.items():
-        if 1 < len(idxs) <= WAVES_PER_WG:
-            assert idxs[0] // WAVES_PER_WG == idxs[-1] // WAVES_PER_WG, key
+    # every (query, head) is covered by its members' items, once per token
+    cover = np.zeros((len(ids), Hkv), dtype=np.int64)
+    for a in it:
+        toks = min(16 * (a[1] + a[2]), a[3]) - 16 * a[1]
+        for q in plan.members[a[7]: a[7] + a[5]]:
+            cover[q, a[4]] += toks
+    assert (cover == np.array(lens)[:, None]).all()
 
 
 def _plan_eval_f64(q, kp, vp, tables, rows, plan, B, scale):
@@ -137,12 +143,12 @@ def _plan_eval_f64(q, kp, vp, tables, rows, plan, B, scale):
     for a in plan.items:
         if a[2] == 0:
             continue
-        row, t0, nt, valid, h, nm, s0 = (int(x) for x in a[:7])
+        row, t0, nt, valid, h, nm, s0, moff = (int(x) for x in a[:8])
         toks = [t for t in range(16 * t0, min(16 * (t0 + nt), valid))]
         K = np.stack([kp[tab[row][t // B], t % B, h] for t in toks]).astype(np.float64)
         V = np.stack([vp[tab[row][t // B], t % B, h] for t in toks]).astype(np.float64)
         for j in range(nm):
-            qi = int(a[7 + j])
+            qi = int(plan.members[moff + j])
             for g in range(G):
                 s = K @ q[qi, h * G + g].astype(np.float64) * scale
                 mx = s.max()
@@ -175,7 +181,9 @@ def test_plan_evaluation_matches_oracle_attention():
     kp = rng.standard_normal((nb, B, Hkv, D))
     vp = rng.standard_normal((nb, B, Hkv, D))
     q = rng.standard_normal((len(ids), Hkv * G, D))
-    plan = build_plan(tables, lens, rows, block_size=B, Hkv=Hkv, G=G, chunk_tiles=2)
-    got = _plan_eval_f64(q, kp, vp, tables, rows, plan, B, D ** -0.5)
     want = paged_decode_f64(q, kp, vp, tables, lens, B)
-    assert np.abs(got - want).max() < 1e-9
+    for min_groups in (1, 2, 99):
+        plan = build_plan(tables, lens, rows, block_size=B, Hkv=Hkv, G=G, chunk_tiles=2, shared_chunk_tiles=3,
+                          shared_min_groups=min_groups)
+        got = _plan_eval_f64(q, kp, vp, tables, rows, plan, B, D ** -0.5)
+        assert np.abs(got - want).max() < 1e-9
