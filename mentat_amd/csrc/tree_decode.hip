@@ -85,7 +85,7 @@ struct TreeParams {
 
 constexpr int kTreeWaves = 8;
 constexpr int kTreeThreads = 64 * kTreeWaves;
-constexpr int kTreePrefetch = 8;        // shared path: tiles in flight per loading thread
+constexpr int kTreePrefetch = 8;        // shared path: tiles in flight per loading thread (even)
 constexpr int kTreeSharedMaxTiles = 16;  // shared path: tiles per task (host-enforced)
 constexpr float kTreeSlack = 8.f;
 
@@ -178,6 +178,57 @@ struct WaveAttn {
     for (int j = 0; j < NT; ++j) o[j] = TMfma<T>::pv(pa, vr[j], o[j]);
   }
 
+  // Two tiles (t, t+1) in one step: two independent S^T chains, one softmax
+  // update over the 32 scores, and O += P.V on 16x16x32 with the k index
+  // 8*lg + i <-> token 4*lg + i of tile t (i < 4) or of tile t+1 (i >= 4):
+  // vb[j] = (V of tile t, V of tile t+1) for dims lr + 16j.
+  __device__ __forceinline__ void tile2(const TreeParams& p, int t, bool ok0, bool ok1, int valid,
+                                        const uint4 (&k0)[KS], const uint4 (&k1)[KS], const uint4 (&vb)[NT]) {
+    f32x4_t s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      s0 = TMfma<T>::qk(k0[s], qo[s], s0);
+      s1 = TMfma<T>::qk(k1[s], qo[s], s1);
+    }
+    const int tok0 = t * 16 + 4 * lg;
+    float sc[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      sc[i] = s0[i] * p.scale_log2;
+      if (!ok0 || tok0 + i >= valid) sc[i] = kNegInf;
+      sc[4 + i] = s1[i] * p.scale_log2;
+      if (!ok1 || tok0 + 16 + i >= valid) sc[4 + i] = kNegInf;
+    }
+    float pm = fmaxf(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])), fmaxf(fmaxf(sc[4], sc[5]), fmaxf(sc[6], sc[7])));
+    const bool grow = (m == kNegInf) ? (pm != kNegInf) : (pm > m + kTreeSlack);
+    if (__builtin_amdgcn_ballot_w64(grow)) {
+      pm = fmaxf(pm, __shfl_xor(pm, 16));
+      pm = fmaxf(pm, __shfl_xor(pm, 32));
+      const float mn = fmaxf(m, pm);
+      const float alpha = (mn == kNegInf) ? 1.f : fast_exp2(m - mn);
+      l *= alpha;
+      m = mn;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float ar = __shfl(alpha, 4 * lg + i);
+#pragma unroll
+        for (int j = 0; j < NT; ++j) o[j][i] *= ar;
+      }
+    }
+    const float ms = (m == kNegInf) ? 0.f : m;
+    f32x4_t pa, pb;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      pa[i] = fast_exp2(sc[i] - ms);
+      pb[i] = fast_exp2(sc[4 + i] - ms);
+    }
+    l += ((pa[0] + pa[1]) + (pa[2] + pa[3])) + ((pb[0] + pb[1]) + (pb[2] + pb[3]));
+    const uint2 ua = TMfma<T>::pack(pa), ub = TMfma<T>::pack(pb);
+    const uint4 pk = make_uint4(ua.x, ua.y, ub.x, ub.y);
+#pragma unroll
+    for (int j = 0; j < NT; ++j) o[j] = TMfma<T>::qk(pk, vb[j], o[j]);
+  }
+
   // Partials of members [0, nmem) of this wave's group; member j -> slot slot0 + j.
   __device__ __forceinline__ void emit(const TreeParams& p, int nmem, int slot0, int G) {
     l += __shfl_xor(l, 16);
@@ -217,6 +268,20 @@ __device__ __forceinline__ void tree_shared(const TreeParams& p, const int32_t* 
   const int t_last = t_first + ntile;
   const int32_t* trow = p.tables + (long)row * p.table_stride;
 
+  // Block ids of the task's tiles, read once into scalar registers (tiles
+  // past the chunk repeat the last one and are masked).
+  int blk[kTreeSharedMaxTiles];
+  unsigned okm = 0;  // bit i: tile i is inside the chunk and its page id is in range
+  static_for<kTreeSharedMaxTiles>([&](auto ic) __attribute__((always_inline)) {
+    constexpr int i = decltype(ic)::value;
+    const int tt = t_first + (i < ntile ? i : ntile - 1);
+    const int pg = min(tt / NSUB, (int)p.table_stride - 1);
+    const int b = tld(trow, pg);
+    const bool ok = i < ntile && b >= 0 && b < p.num_blocks;
+    blk[i] = ok ? b : 0;
+    okm |= ok ? (1u << i) : 0u;
+  });
+
   // This thread's 16-byte piece of every tile: waves [0, 2D/64) carry K,
   // waves [2D/64, 4D/64) carry V, the rest carry nothing (D = 64).
   const bool loader = wave * 64 < 4 * D;
@@ -233,24 +298,27 @@ __device__ __forceinline__ void tree_shared(const TreeParams& p, const int32_t* 
     loff = L::KST + d * L::VRS + h * 16;
   }
   const S* base = (const S*)(is_k ? p.k : p.v);
-  auto issue = [&](int t) __attribute__((always_inline)) -> uint4 {
-    const int page = t / NSUB, sub = t - page * NSUB;
-    int blk = -1;
-    if (t < t_last && page < p.table_stride) blk = tld(trow, page);
-    const bool okb = blk >= 0 && blk < p.num_blocks && loader;
-    const long ph = ((okb ? (long)blk : 0L) * p.Hkv + head) * (long)(B * D);
-    const __amdgpu_buffer_rsrc_t r = trsrc(base + ph, okb ? B * D * (int)sizeof(S) : 0);
+  // Tile i of the task (zeros, with no memory traffic, when masked).
+  auto issue = [&](auto ic) __attribute__((always_inline)) -> uint4 {
+    constexpr int i = decltype(ic)::value;
+    const int t = t_first + i;
+    const int sub = t - (t / NSUB) * NSUB;
+    const bool ok = loader && ((okm >> i) & 1u);
+    const long ph = ((long)blk[i] * p.Hkv + head) * (long)(B * D);
+    const __amdgpu_buffer_rsrc_t r = trsrc(base + ph, ok ? B * D * (int)sizeof(S) : 0);
     const int soff = (is_k ? sub * 16 * D : sub * 16) * (int)sizeof(S);
     return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, goff, soff, 0));
   };
 
-  // The tile loop is fully unrolled (ntile <= kTreeSharedMaxTiles): with no
-  // back edge, every wait for a prefetched tile counts exactly the loads
-  // issued after it.
-  uint4 pf[kTreePrefetch];
+  // Steps of two tiles; tiles 2s, 2s+1 go to LDS stage s & 1. kTreePrefetch
+  // tiles are in flight ahead of the one being written (ring of kTreePrefetch
+  // + 2 registers, so a step's loads never overwrite what it writes). The
+  // loop is fully unrolled: with no back edge every wait counts exactly.
+  constexpr int R = kTreePrefetch + 2;
+  uint4 pf[R];
   static_for<kTreePrefetch>([&](auto ic) __attribute__((always_inline)) {
     constexpr int i = decltype(ic)::value;
-    pf[i] = issue(t_first + i);
+    pf[i] = issue(ic);
   });
   // The query loads (member index, then q) go out after the first tiles.
   const int g0 = wave * MG;
@@ -261,35 +329,44 @@ __device__ __forceinline__ void tree_shared(const TreeParams& p, const int32_t* 
     const int qidx = (active && g0 + cm < nmem) ? p.members[moff + g0 + cm] : -1;
     w.init(p, lane, qidx, head, G);
   }
-  static_for<kTreeSharedMaxTiles>([&](auto ic) __attribute__((always_inline)) {
-    constexpr int i = decltype(ic)::value;
-    if (i < ntile) {
-      const int t = t_first + i;
-      char* stg = lds + (i & 1) * L::STAGE;
-      const uint4 cur = pf[i % kTreePrefetch];
+  static_for<kTreeSharedMaxTiles / 2>([&](auto sc_) __attribute__((always_inline)) {
+    constexpr int st = decltype(sc_)::value;
+    constexpr int i0 = 2 * st;
+    if (i0 < ntile) {
+      if constexpr (i0 + kTreePrefetch < kTreeSharedMaxTiles)
+        pf[(i0 + kTreePrefetch) % R] = issue(std::integral_constant<int, i0 + kTreePrefetch>{});
+      if constexpr (i0 + 1 + kTreePrefetch < kTreeSharedMaxTiles)
+        pf[(i0 + 1 + kTreePrefetch) % R] = issue(std::integral_constant<int, i0 + 1 + kTreePrefetch>{});
+      char* stg = lds + (st & 1) * 2 * L::STAGE;
       if (loader) {
-        if (is_k) {
-          *(uint4*)__builtin_assume_aligned(stg + loff, 16) = cur;
-        } else {
-          *(uint2*)__builtin_assume_aligned(stg + loff, 8) = make_uint2(cur.x, cur.y);
-          *(uint2*)__builtin_assume_aligned(stg + loff + 8, 8) = make_uint2(cur.z, cur.w);
-        }
+        static_for<2>([&](auto hc) __attribute__((always_inline)) {
+          constexpr int h = decltype(hc)::value;
+          const uint4 cur = pf[(i0 + h) % R];
+          char* dst = stg + h * L::STAGE + loff;
+          if (is_k) {
+            *(uint4*)__builtin_assume_aligned(dst, 16) = cur;
+          } else {
+            *(uint2*)__builtin_assume_aligned(dst, 8) = make_uint2(cur.x, cur.y);
+            *(uint2*)__builtin_assume_aligned(dst + 8, 8) = make_uint2(cur.z, cur.w);
+          }
+        });
       }
-      if constexpr (i + kTreePrefetch < kTreeSharedMaxTiles) pf[i % kTreePrefetch] = issue(t + kTreePrefetch);
       __syncthreads();
       if (active) {
-        const int page = t / NSUB;
-        const int blk = page < p.table_stride ? tld(trow, page) : -1;
-        const bool okb = blk >= 0 && blk < p.num_blocks;
-        uint4 kr[KS];
-        uint2 vr[NT];
+        uint4 k0[KS], k1[KS], vb[NT];
 #pragma unroll
-        for (int s = 0; s < KS; ++s)
-          kr[s] = *(const uint4*)__builtin_assume_aligned(stg + w.lr * L::KRS + (4 * s + w.lg) * 16, 16);
+        for (int s = 0; s < KS; ++s) {
+          k0[s] = *(const uint4*)__builtin_assume_aligned(stg + w.lr * L::KRS + (4 * s + w.lg) * 16, 16);
+          k1[s] = *(const uint4*)__builtin_assume_aligned(stg + L::STAGE + w.lr * L::KRS + (4 * s + w.lg) * 16, 16);
+        }
 #pragma unroll
-        for (int j = 0; j < NT; ++j)
-          vr[j] = *(const uint2*)__builtin_assume_aligned(stg + L::KST + (w.lr + 16 * j) * L::VRS + w.lg * 8, 8);
-        w.tile(p, t, okb, valid, kr, vr);
+        for (int j = 0; j < NT; ++j) {
+          const int vo = L::KST + (w.lr + 16 * j) * L::VRS + w.lg * 8;
+          const uint2 a0 = *(const uint2*)__builtin_assume_aligned(stg + vo, 8);
+          const uint2 a1 = *(const uint2*)__builtin_assume_aligned(stg + L::STAGE + vo, 8);
+          vb[j] = make_uint4(a0.x, a0.y, a1.x, a1.y);
+        }
+        w.tile2(p, t_first + i0, (okm >> i0) & 1u, (okm >> (i0 + 1)) & 1u, valid, k0, k1, vb);
       }
     }
   });
@@ -353,7 +430,7 @@ __device__ __forceinline__ void tree_solo(const TreeParams& p, const int32_t* it
 
 template <typename T, int D, int G, int B>
 __global__ __launch_bounds__(kTreeThreads) void tree_decode_kernel(TreeParams p) {
-  __shared__ uint4 lds_words[2 * TileLds<D>::STAGE / 16];
+  __shared__ uint4 lds_words[4 * TileLds<D>::STAGE / 16];  // 2 stages x 2 tiles
   char* lds = (char*)lds_words;
   const int bid = blockIdx.x;
   if (bid < p.n_shared) {
