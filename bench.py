@@ -1,18 +1,23 @@
 #!/usr/bin/env python3
 """Benchmark of the branching-decode hot path on one MI355X.
 
-Workload: paged decode attention at Llama-3-8B attention shapes (bf16, 32 q /
-8 kv heads, head_dim 128, page size 16, 64 sequences with contexts uniform in
-[512, 4096], block tables from a seeded permutation of a 65,536-page pool,
-Q/K/V ~ N(0,1), scale 1/sqrt(128)). One step = one decode call over the batch
-with every input already resident in HBM.
+Default workload (--workload decode): paged decode attention at Llama-3-8B
+attention shapes (bf16, 32 q / 8 kv heads, head_dim 128, page size 16, 64
+sequences with contexts uniform in [512, 4096], block tables from a seeded
+permutation of a 65,536-page pool, Q/K/V ~ N(0,1), scale 1/sqrt(128)). One
+step = one decode call over the batch with every input already resident in HBM.
 
 Prints one JSON line with the whole-job throughput (achieved HBM GB/s of
 algorithmic bytes), the roofline fraction against MI355X's 8 TB/s, and the
-reference's CPU decode path (gather + per-sequence SDPA, torch on the host
-cores) timed beside it on the same inputs.
+reference's CPU path timed beside it on the same inputs.
 
-  python bench.py [--gpus 1] [--steps K] [--warmup W]
+Other workloads (their own JSON line, same fields):
+  --workload tree   prefix-tree decode at Qwen3-8B attention shapes: 4 trees
+                    of 32 leaves over 2048-token prompts (GB/s of unique bytes)
+  --workload rows   fused entropy gate + temperature/top-p sampling over
+                    [256, 151936] bf16 logits (GB/s of logits bytes)
+
+  python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload decode|tree|rows]
 """
 from __future__ import annotations
 
@@ -76,11 +81,266 @@ def _cpu_baseline(batch, min_seconds: float):
     }
 
 
+def _time_steps(step, steps: int, warmup: int, dev):
+    """Untimed warmup, then `steps` calls bracketed by HIP events on the launch stream."""
+    import torch
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream(dev)  # the stream the kernels are launched on
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    evs[0].record(stream)
+    for i in range(steps):
+        step()
+        evs[i + 1].record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    per = [evs[i].elapsed_time(evs[i + 1]) for i in range(steps)]
+    ms = evs[0].elapsed_time(evs[-1]) / steps
+    print(f"bench: {steps} steps, mean {ms:.4f} ms, median {statistics.median(per):.4f} ms, wall {wall:.3f} s",
+          file=sys.stderr, flush=True)
+    return ms
+
+
+def _line(args, value_gbs: float, ms: float, config: dict, cpu, traffic, extra: dict | None = None) -> dict:
+    out = {
+        "metric": METRIC,
+        "value": round(value_gbs, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded; see config)",
+        "config": config,
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(value_gbs, 2),
+            "peak": PEAK_HBM_GBS,
+            "unit": "GB/s",
+            "frac": round(value_gbs / PEAK_HBM_GBS, 4),
+            "traffic": traffic,
+        },
+        "cpu_baseline": cpu,
+    }
+    if extra:
+        out.update(extra)
+    return out
+
+
+def run_decode(args, dev) -> dict:
+    import torch
+
+    from mentat_amd import ops
+    from mentat_amd._lib import LAYOUT_NATIVE
+    from mentat_amd.workloads import paged_decode_batch
+
+    print("bench: building the paged decode workload", file=sys.stderr, flush=True)
+    b = paged_decode_batch(device=dev, seed=0, layout=LAYOUT_NATIVE)
+    nbytes = b.algorithmic_bytes()
+    out = torch.empty_like(b.q)
+    # Two copies of Q and the K/V stores (same tables), used alternately: each
+    # step re-reads data last touched ~1.2 GB of traffic earlier, beyond the
+    # 256 MB Infinity Cache.
+    g = torch.Generator(device=dev).manual_seed(1)
+    sets = [(b.q, b.k_store, b.v_store),
+            (torch.randn(b.q.shape, generator=g, device=dev).to(b.q.dtype), b.k_store.clone(), b.v_store.clone())]
+    state = {"i": 0}
+
+    def step():
+        q, ks, vs = sets[state["i"] & 1]
+        state["i"] += 1
+        ops.paged_decode(q, ks, vs, layout=b.layout, block_tables=b.block_tables,
+                         seq_lens=b.seq_lens, max_seqlen=b.max_seqlen, scale=b.scale, out=out)
+
+    ms = _time_steps(step, args.steps, args.warmup, dev)
+    cpu = None
+    if not args.no_cpu_baseline:
+        print("bench: timing the CPU baseline", file=sys.stderr, flush=True)
+        cpu = _cpu_baseline(b, args.cpu_seconds)
+    config = {
+        "workload": "paged decode attention, Llama-3-8B attention shapes",
+        "num_seqs": b.q.shape[0],
+        "q_heads": b.q.shape[1],
+        "kv_heads": b.k_pool.shape[2],
+        "head_dim": b.q.shape[2],
+        "page_size": b.block_size,
+        "context": "uniform [512, 4096], seed 0",
+        "sum_context_tokens": sum(b.lens),
+        "pool_pages": b.k_pool.shape[0],
+        "pool_layout": "native (K [page][kv head][slot][dim], V [page][kv head][dim][slot])",
+        "algorithmic_bytes_per_step": nbytes,
+        "rotation": "2 copies of Q and the K/V stores used alternately",
+    }
+    line = _line(args, nbytes / (ms * 1e-3) / 1e9, ms, config, cpu, _measured_traffic(),
+                 {"decode_calls_per_s": round(1e3 / ms, 1)})
+    line["data"] = "synthetic (seeded N(0,1) Q/K/V, seeded ragged contexts and page permutation)"
+    return line
+
+
+def run_tree(args, dev) -> dict:
+    import torch
+
+    from mentat_amd import ops
+    from mentat_amd._lib import LAYOUT_NATIVE
+    from mentat_amd.tree_plan import build_plan
+    from mentat_amd.workloads import prefix_tree_batch
+
+    print("bench: building the prefix-tree workload", file=sys.stderr, flush=True)
+    tb = prefix_tree_batch(device=dev, seed=0)
+    G = tb.q.shape[1] // tb.k_store.shape[1]
+    t0 = time.perf_counter()
+    plan = build_plan(tb.tables, tb.lens, tb.rows, block_size=tb.block_size, Hkv=tb.k_store.shape[1], G=G)
+    plan_ms = (time.perf_counter() - t0) * 1e3
+    out = torch.empty_like(tb.q)
+    # Four copies of the stores (same trees and tables), used in turn: each
+    # step re-reads data last touched ~240 MB of unique traffic earlier, so the
+    # 256 MB Infinity Cache cannot serve the 80 MB working set from one step to
+    # the next.
+    sets = [(tb.k_store, tb.v_store)] + [(tb.k_store.clone(), tb.v_store.clone()) for _ in range(3)]
+    state = {"i": 0}
+
+    def step():
+        ks, vs = sets[state["i"] % len(sets)]
+        state["i"] += 1
+        ops.tree_decode(tb.q, ks, vs, block_tables=tb.block_tables, plan=plan, scale=tb.scale, out=out)
+
+    ms = _time_steps(step, args.steps, args.warmup, dev)
+    rows_t = torch.tensor(tb.rows, dtype=torch.int32, device=dev)
+
+    def paged():
+        ks, vs = sets[state["i"] % len(sets)]
+        state["i"] += 1
+        ops.paged_decode(tb.q, ks, vs, max_seqlen=max(tb.lens), block_tables=tb.block_tables,
+                         seq_lens=tb.seq_lens, seq_rows=rows_t, scale=tb.scale, layout=LAYOUT_NATIVE)
+
+    paged_ms = _time_steps(paged, args.steps, args.warmup, dev)
+    ub, lb = tb.unique_bytes(), tb.logical_bytes()
+    cpu = None
+    if not args.no_cpu_baseline:
+        print("bench: timing the CPU baseline", file=sys.stderr, flush=True)
+        cpu = _cpu_baseline_tree(tb, args.cpu_seconds)
+    config = {
+        "workload": "prefix-tree decode attention, Qwen3-8B attention shapes",
+        "trees": 4, "leaves_per_tree": 32, "prompt_tokens": 2048, "private_tokens": "0..512 per leaf",
+        "q_heads": tb.q.shape[1], "kv_heads": tb.k_store.shape[1], "head_dim": tb.q.shape[2],
+        "page_size": tb.block_size, "qk_rmsnorm": True,
+        "unique_tokens": tb.unique_tokens(), "logical_tokens": tb.logical_tokens(),
+        "unique_bytes_per_step": ub, "logical_bytes_per_step": lb,
+        "rotation": "4 copies of the K/V stores used in turn",
+        "plan": {"shared_tasks": plan.n_shared, "solo_items": plan.n_solo, "partial_slots": plan.n_slots,
+                 "host_build_ms": round(plan_ms, 2)},
+    }
+    line = _line(args, ub / (ms * 1e-3) / 1e9, ms, config, cpu, None, {
+        "logical_gbs": round(lb / (ms * 1e-3) / 1e9, 1),
+        "paged_decode_same_batch_ms": round(paged_ms, 5),
+        "speedup_vs_paged_decode": round(paged_ms / ms, 2),
+    })
+    line["data"] = "synthetic (seeded trees grown through the paged cache manager; RMS-normed N(0,1) q/k, N(0,1) v)"
+    return line
+
+
+def _cpu_baseline_tree(tb, min_seconds: float):
+    """The reference's CPU decode path (no prefix sharing) on a sample of the leaves."""
+    import torch
+
+    from oracle.attention import reference_cpu_decode
+
+    torch.set_num_threads(max(1, int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))))
+    sample = list(range(0, len(tb.seq_ids), 8))  # 16 of the 128 leaves
+    flat = [p for i in sample for p in tb.tables[i]]
+    kp = tb.k_store.permute(0, 2, 1, 3)
+    vp = tb.v_store.permute(0, 3, 1, 2)
+    idx = torch.tensor(flat, dtype=torch.long, device=tb.k_store.device)
+    k_host, v_host = kp[idx].contiguous().cpu(), vp[idx].contiguous().cpu()
+    tables, off = [], 0
+    for i in sample:
+        tables.append(list(range(off, off + len(tb.tables[i]))))
+        off += len(tb.tables[i])
+    q_host = tb.q[sample].cpu()
+    lens = [tb.lens[i] for i in sample]
+    reps, total = 0, 0.0
+    while total < min_seconds or reps < 1:
+        t0 = time.perf_counter()
+        reference_cpu_decode(q_host, k_host, v_host, tables, lens, tb.block_size)
+        total += time.perf_counter() - t0
+        reps += 1
+    per = total / reps
+    Hkv, D = tb.k_store.shape[1], tb.q.shape[2]
+    nbytes = sum(lens) * Hkv * D * 2 * 2
+    return {"value": round(nbytes / per / 1e9, 3), "unit": "GB/s (logical bytes)", "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": f"16 of the 128 leaves, {reps} repetitions ({total:.1f} s): per-leaf gather + SDPA, bf16, "
+                      f"torch CPU (the reference reads every leaf's full context)"}
+
+
+def run_rows(args, dev) -> dict:
+    import torch
+
+    from mentat_amd import ops
+    from mentat_amd.workloads import sampling_logits
+
+    print("bench: building the sampling workload", file=sys.stderr, flush=True)
+    x, sig = sampling_logits(device=dev, seed=0)
+    R, V = x.shape
+    nbytes = x.numel() * x.element_size()
+    T, TOP_P, THR = 0.7, 0.9, 3.0
+    # Four logits sets (seeds 0..3) used in turn, so the 256 MB Infinity Cache
+    # cannot hold a step's 78 MB until the next time it is read.
+    xs = [x] + [sampling_logits(device=dev, seed=s)[0] for s in (1, 2, 3)]
+    state = {"i": 0}
+
+    def step():
+        ops.row_stats(xs[state["i"] % len(xs)], temperature=T, gate_threshold=THR, sample=True,
+                      sample_temperature=T, top_p=TOP_P, seed=1234, step=state["i"], pen_stats=False)
+        state["i"] += 1
+
+    ms = _time_steps(step, args.steps, args.warmup, dev)
+    st = ops.row_stats(x, temperature=T, gate_threshold=THR, sample=True, sample_temperature=T, top_p=TOP_P,
+                       seed=1234, step=0, pen_stats=False)
+    gated = int(st.gate.sum().item())
+    cpu = None
+    if not args.no_cpu_baseline:
+        from oracle.sampling import reference_cpu_rows
+
+        torch.set_num_threads(max(1, int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))))
+        xs = x[:32].cpu()
+        reps, total = 0, 0.0
+        while total < args.cpu_seconds or reps < 1:
+            t0 = time.perf_counter()
+            reference_cpu_rows(xs, T, TOP_P, THR)
+            total += time.perf_counter() - t0
+            reps += 1
+        per = total / reps
+        cpu = {"value": round(xs.numel() * 2 / per / 1e9, 3), "unit": "GB/s", "cores": torch.get_num_threads(),
+               "kind": "port",
+               "sample": f"32 of the 256 rows, {reps} repetitions ({total:.1f} s): compute_entropy + HF top-p "
+                         f"(sort, cumsum, multinomial) per row, bf16, torch CPU"}
+    config = {
+        "workload": "fused entropy gate + temperature/top-p sampling",
+        "rows": R, "vocab": V, "sigma": "uniform [0.5, 4] per row", "temperature": T, "top_p": TOP_P,
+        "gate_nats": THR, "gated_rows_seed0": gated, "sampler": "Philox4x32-10, seed 1234, step = call index",
+        "rotation": "4 logits sets (seeds 0-3) used in turn",
+        "logits_bytes_per_step": nbytes,
+    }
+    line = _line(args, nbytes / (ms * 1e-3) / 1e9, ms, config, cpu, None, {"rows_per_s": round(R * 1e3 / ms, 1)})
+    line["data"] = "synthetic (seeded N(0, sigma_r) logits)"
+    return line
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--workload", choices=("decode", "tree", "rows"), default="decode")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="minimum host time spent on the CPU baseline")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -95,86 +355,10 @@ def main() -> int:
 
     import torch
 
-    from mentat_amd import ops
-    from mentat_amd._lib import LAYOUT_NATIVE
-    from mentat_amd.workloads import paged_decode_batch
-
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
-    print("bench: building the workload", file=sys.stderr, flush=True)
-    b = paged_decode_batch(device=dev, seed=0, layout=LAYOUT_NATIVE)
-    nbytes = b.algorithmic_bytes()
-    out = torch.empty_like(b.q)
-
-    def step():
-        ops.paged_decode(b.q, b.k_store, b.v_store, layout=b.layout, block_tables=b.block_tables,
-                         seq_lens=b.seq_lens, max_seqlen=b.max_seqlen, scale=b.scale, out=out)
-
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    print("bench: warmup done", file=sys.stderr, flush=True)
-
-    stream = torch.cuda.current_stream(dev)  # the stream the kernels are launched on
-    evs = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    evs[0].record(stream)
-    for i in range(args.steps):
-        step()
-        evs[i + 1].record(stream)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    per_step_ms = [evs[i].elapsed_time(evs[i + 1]) for i in range(args.steps)]
-    total_ms = evs[0].elapsed_time(evs[-1])
-    ms = total_ms / args.steps
-    achieved = nbytes / (ms * 1e-3) / 1e9
-    print(f"bench: {args.steps} steps, mean {ms:.4f} ms, median {statistics.median(per_step_ms):.4f} ms, "
-          f"wall {wall:.3f} s", file=sys.stderr, flush=True)
-
-    cpu = None
-    if not args.no_cpu_baseline:
-        print("bench: timing the CPU baseline", file=sys.stderr, flush=True)
-        cpu = _cpu_baseline(b, args.cpu_seconds)
-
-    result = {
-        "metric": METRIC,
-        "value": round(achieved, 2),
-        "unit": "GB/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(ms, 5),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "bf16",
-        "data": "synthetic (seeded N(0,1) Q/K/V, seeded ragged contexts and page permutation)",
-        "config": {
-            "workload": "paged decode attention, Llama-3-8B attention shapes",
-            "num_seqs": b.q.shape[0],
-            "q_heads": b.q.shape[1],
-            "kv_heads": b.k_pool.shape[2],
-            "head_dim": b.q.shape[2],
-            "page_size": b.block_size,
-            "context": "uniform [512, 4096], seed 0",
-            "sum_context_tokens": sum(b.lens),
-            "pool_pages": b.k_pool.shape[0],
-            "pool_layout": "native (K [page][kv head][slot][dim], V [page][kv head][dim][slot])",
-            "algorithmic_bytes_per_step": nbytes,
-        },
-        "roofline": {
-            "bound": "hbm",
-            "achieved": round(achieved, 2),
-            "peak": PEAK_HBM_GBS,
-            "unit": "GB/s",
-            "frac": round(achieved / PEAK_HBM_GBS, 4),
-            "traffic": _measured_traffic(),
-        },
-        "cpu_baseline": cpu,
-        "decode_calls_per_s": round(1e3 / ms, 1),
-    }
-    print(json.dumps(result), flush=True)
+    run = {"decode": run_decode, "tree": run_tree, "rows": run_rows}[args.workload]
+    print(json.dumps(run(args, dev)), flush=True)
     return 0
 
 

@@ -11,7 +11,12 @@
  *      MENTAT_ESPACE (-3) the caller's workspace is smaller than required
  *      > 0                a hipError_t returned by the launch
  * The library never allocates device memory: workspaces are passed in by the
- * caller, sized with the matching *_workspace_bytes() query.
+ * caller, sized with the matching *_workspace_bytes() query. Every workspace
+ * begins with MENTAT_WORKSPACE_RESERVED bytes of arrival counters (native
+ * paged decode) that must be zero before the workspace's first use; every
+ * call leaves them zero and keeps its own data after them, so one zero-filled
+ * workspace per stream can serve every entry point. Calls that share a
+ * workspace must be ordered (the same stream).
  *
  * Pools hold num_blocks pages of block_size tokens x num_kv_heads x head_dim
  * elements in the model dtype, in one of two layouts (MENTAT_LAYOUT_* below);
@@ -35,6 +40,8 @@ extern "C" {
 #define MENTAT_EINVAL (-1)
 #define MENTAT_EUNSUP (-2)
 #define MENTAT_ESPACE (-3)
+
+#define MENTAT_WORKSPACE_RESERVED 262144
 
 #define MENTAT_F32 0
 #define MENTAT_F16 1

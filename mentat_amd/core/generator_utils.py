@@ -158,6 +158,23 @@ def apply_repetition_penalty(logits: torch.Tensor, token_ids: list[int], penalty
     return logits
 
 
+def _find_blocked_tokens(token_ids: list[int], max_n: int) -> set[int]:
+    """Tokens that would repeat an n-gram (2 <= n <= max_n): wherever the last
+    n-1 tokens occurred earlier, the token that followed them there
+    (core/generator_utils.py:233-244; imported by the reference's generator)."""
+    blocked: set[int] = set()
+    total = len(token_ids)
+    for n in range(2, max_n + 1):
+        k = n - 1
+        if total < n:
+            continue
+        tail = token_ids[total - k:]
+        for start in range(total - k):
+            if token_ids[start:start + k] == tail:
+                blocked.add(token_ids[start + k])
+    return blocked
+
+
 def adaptive_threshold(base_val: float, max_active: int, current_active: int) -> float:
     util = current_active / max(max_active, 1)
     return base_val * (1.0 + 2.0 * util * util)

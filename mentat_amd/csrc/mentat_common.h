@@ -21,6 +21,14 @@ __device__ __forceinline__ void static_for(F&& f) {
   static_for_impl(f, std::make_integer_sequence<int, N>{});
 }
 
+// Every workspace passed to this library begins with MENTAT_WORKSPACE_RESERVED
+// bytes of arrival counters for the native paged decode (one int32 per
+// (sequence, kv head) unit). They must be zero before a workspace's first use;
+// every call leaves them zero, and every entry point keeps its own data after
+// them, so one workspace can serve all entry points on a stream.
+constexpr size_t kWsReserved = MENTAT_WORKSPACE_RESERVED;
+constexpr int kMaxNativeUnits = (int)(kWsReserved / sizeof(int32_t));
+
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 constexpr float kNegInf = -__builtin_huge_valf();

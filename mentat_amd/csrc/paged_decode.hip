@@ -300,7 +300,7 @@ extern "C" size_t mentat_paged_decode_workspace_bytes(int layout, int N, int Hq,
   const int chunk = chunk_tokens > 0 ? chunk_tokens : auto_chunk(N, Hkv, block_size, max_seqlen);
   const int mc = ceil_div(max_seqlen, chunk);
   if (mc <= 1) return 0;
-  return (size_t)N * Hq * mc * (D + 2) * sizeof(float);
+  return kWsReserved + (size_t)N * Hq * mc * (D + 2) * sizeof(float);
 }
 
 extern "C" int mentat_paged_decode(int layout, const void* q, const void* k_cache, const void* v_cache,
@@ -335,9 +335,9 @@ extern "C" int mentat_paged_decode(int layout, const void* q, const void* k_cach
   p.scale_log2 = scale * kLog2e;
   p.ws_acc = nullptr; p.ws_ml = nullptr;
   if (p.max_chunks > 1) {
-    const size_t need = (size_t)N * Hq * p.max_chunks * (D + 2) * sizeof(float);
+    const size_t need = kWsReserved + (size_t)N * Hq * p.max_chunks * (D + 2) * sizeof(float);
     if (!workspace || workspace_bytes < need) return MENTAT_ESPACE;
-    p.ws_acc = (float*)workspace;
+    p.ws_acc = (float*)((char*)workspace + kWsReserved);
     p.ws_ml = p.ws_acc + (size_t)N * Hq * p.max_chunks * D;
   }
   const int G = Hq / Hkv;

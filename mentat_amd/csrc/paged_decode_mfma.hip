@@ -77,7 +77,7 @@ struct NativeParams {
   void* out;
   float* ws_o;       // [slots][G][D]
   float* ws_ml;      // [slots][G][2]
-  int32_t* ws_meta;  // [0] tiles per wave, [1 .. N+1] tile prefix over sequences
+  int32_t* ctr;      // [N*Hkv] arrival counters of split units (zero between calls)
   int N, Hq, Hkv, B, W;
   float scale_log2;
 };
@@ -139,6 +139,48 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, in
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes, 0x00020000);
 }
 
+// Split units are merged inside the kernel by the wavefront whose piece
+// arrives last. Pieces and counters are written and read with device-coherent
+// (agent-scope) accesses, which go past the per-XCD L2 caches, so no cache-wide
+// write-back or invalidate is needed: a piece's stores complete (s_waitcnt)
+// before its arrival is counted, and the merging wave reads the pieces only
+// after its own arrival returned the full count.
+__device__ __forceinline__ void put_shared(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float get_shared(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Pieces are the partial slots unit + w of waves w0..w1; lane l owns the
+// E = G*D/64 consecutive outputs starting at l*E of the unit's [G][D] block.
+template <typename T, int D, int G>
+__device__ __forceinline__ void merge_unit(const NativeParams& p, int seq, int head, long unit, int w0, int w1,
+                                           int lane) {
+  constexpr int E = G * D / 64;
+  static_assert(E >= 1, "merge lane split");
+  const int g = (lane * E) / D;
+  const int d0 = (lane * E) - g * D;
+  float M = kNegInf;
+  for (int w = w0; w <= w1; ++w) M = fmaxf(M, get_shared(p.ws_ml + ((unit + w) * G + g) * 2));
+  const float ms = (M == kNegInf) ? 0.f : M;
+  float L = 0.f, acc[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) acc[e] = 0.f;
+  for (int w = w0; w <= w1; ++w) {
+    const long slot = unit + w;
+    const float c = fast_exp2(get_shared(p.ws_ml + (slot * G + g) * 2) - ms);
+    L += get_shared(p.ws_ml + (slot * G + g) * 2 + 1) * c;
+    const float* wo = p.ws_o + (slot * G + g) * D + d0;
+#pragma unroll
+    for (int e = 0; e < E; ++e) acc[e] += get_shared(wo + e) * c;
+  }
+  const float inv = L > 0.f ? 1.f / L : 0.f;
+  const long ob = ((long)seq * p.Hq + (long)head * G + g) * D + d0;
+#pragma unroll
+  for (int e = 0; e < E; ++e) Elem<T>::store1(p.out, ob + e, acc[e] * inv);
+}
+
 template <typename T, int D, int G, int B>
 __global__ __launch_bounds__(kNativeThreads) void paged_decode_mfma_kernel(NativeParams p) {
   static_assert(D % 32 == 0 && G >= 1 && G <= 16 && B % 16 == 0, "tile shape");
@@ -153,12 +195,14 @@ __global__ __launch_bounds__(kNativeThreads) void paged_decode_mfma_kernel(Nativ
 
   const int T_total = uniform(p.Hkv * s_prefix[p.N]);
   const int tpw = (T_total + p.W - 1) / p.W;
-  if (blockIdx.x == 0) {
-    if (threadIdx.x == 0) p.ws_meta[0] = tpw;
-    for (int s = threadIdx.x; s <= p.N; s += kNativeThreads) p.ws_meta[1 + s] = s_prefix[s];
-  }
   const int lane = threadIdx.x & 63;
   const int wv = uniform(blockIdx.x * (kNativeThreads / 64) + (threadIdx.x >> 6));
+  // Sequences without cached tokens get zeros (no tile covers them).
+  for (int s = wv; s < p.N; s += p.W) {
+    if (s_prefix[s + 1] == s_prefix[s]) {
+      for (int e = lane; e < p.Hq * D; e += 64) Elem<T>::store1(p.out, (long)s * p.Hq * D + e, 0.f);
+    }
+  }
   int f = wv * tpw;
   const int fend = min(T_total, f + tpw);
   if (f >= fend) return;
@@ -319,12 +363,23 @@ __global__ __launch_bounds__(kNativeThreads) void paged_decode_mfma_kernel(Nativ
         if (qrow < G) {
           float* wo = p.ws_o + (slot * G + qrow) * D + lr;
 #pragma unroll
-          for (int j = 0; j < NT; ++j) wo[16 * j] = o[j][i];
+          for (int j = 0; j < NT; ++j) put_shared(wo + 16 * j, o[j][i]);
         }
       }
       if (lane < G) {
-        p.ws_ml[(slot * G + lane) * 2] = m;
-        p.ws_ml[(slot * G + lane) * 2 + 1] = l;
+        put_shared(p.ws_ml + (slot * G + lane) * 2, m);
+        put_shared(p.ws_ml + (slot * G + lane) * 2 + 1, l);
+      }
+      // Arrival: the piece's stores complete, then it is counted; the unit's
+      // last piece merges them all.
+      const int w0 = ustart / tpw, w1 = (uend - 1) / tpw;
+      __builtin_amdgcn_s_waitcnt(0);
+      int old = 0;
+      if (lane == 0) old = __hip_atomic_fetch_add(p.ctr + unit, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      old = __shfl(old, 0);
+      if (old == w1 - w0) {
+        merge_unit<T, D, G>(p, seq, head, unit, w0, w1, lane);
+        if (lane == 0) __hip_atomic_store(p.ctr + unit, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
     }
 
@@ -345,65 +400,9 @@ __global__ __launch_bounds__(kNativeThreads) void paged_decode_mfma_kernel(Nativ
   }
 }
 
-// Merge split units; write zeros for sequences without cached tokens.
-// grid: N * Hkv workgroups (one per unit) of one wavefront; lane l owns the
-// E = G*D/64 consecutive outputs starting at l*E of the unit's [G][D] block.
-// Pieces are merged online (running max, sum and rescaled accumulator).
-template <typename T, int D, int G>
-__global__ __launch_bounds__(64) void native_combine_kernel(NativeParams p) {
-  constexpr int E = G * D / 64;
-  static_assert(E >= 1 && (E % 2 == 0 || E == 1), "combine lane split");
-  const long unit = blockIdx.x;
-  const int head = (int)(unit % p.Hkv);
-  const int seq = (int)(unit / p.Hkv);
-  if (seq >= p.N) return;
-  const int lane = threadIdx.x;
-  const int g = (lane * E) / D;
-  const int d0 = (lane * E) - g * D;
-  const long ob = ((long)seq * p.Hq + (long)head * G + g) * D + d0;
-  const int pre = scalar_load(p.ws_meta + 1, seq);
-  const int nt = scalar_load(p.ws_meta + 1, seq + 1) - pre;
-  const int tpw = scalar_load(p.ws_meta, 0);
-  if (nt == 0) {
-#pragma unroll
-    for (int e = 0; e < E; ++e) Elem<T>::store1(p.out, ob + e, 0.f);
-    return;
-  }
-  const int ustart = p.Hkv * pre + head * nt;
-  const int w0 = ustart / tpw;
-  const int w1 = (ustart + nt - 1) / tpw;
-  if (w0 == w1) return;  // written by the main kernel
-  float M = kNegInf, L = 0.f, acc[E];
-#pragma unroll
-  for (int e = 0; e < E; ++e) acc[e] = 0.f;
-  for (int w = w0; w <= w1; ++w) {
-    const long slot = unit + w;
-    const float mp = p.ws_ml[(slot * G + g) * 2];
-    const float lp = p.ws_ml[(slot * G + g) * 2 + 1];
-    float op[E];
-    const float* wo = p.ws_o + (slot * G + g) * D + d0;
-#pragma unroll
-    for (int e = 0; e < E; ++e) op[e] = wo[e];
-    const float mn = fmaxf(M, mp);
-    const float ms = (mn == kNegInf) ? 0.f : mn;
-    const float a = fast_exp2(M - ms), b = fast_exp2(mp - ms);
-    L = L * a + lp * b;
-#pragma unroll
-    for (int e = 0; e < E; ++e) acc[e] = acc[e] * a + op[e] * b;
-    M = mn;
-  }
-  const float inv = L > 0.f ? 1.f / L : 0.f;
-#pragma unroll
-  for (int e = 0; e < E; ++e) Elem<T>::store1(p.out, ob + e, acc[e] * inv);
-}
-
 template <typename T, int D, int G, int B>
 static int launch_native(const NativeParams& p, hipStream_t stream) {
   hipLaunchKernelGGL((paged_decode_mfma_kernel<T, D, G, B>), dim3(p.W / 4), dim3(kNativeThreads), 0, stream, p);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return (int)e;
-  hipLaunchKernelGGL((native_combine_kernel<T, D, G>), dim3((unsigned)((long)p.N * p.Hkv)), dim3(64), 0,
-                     stream, p);
   return (int)hipGetLastError();
 }
 
@@ -460,20 +459,20 @@ static int persistent_waves() {
 
 using namespace mentat;
 
-// Workspace of the native path: partial slots (units + waves), metadata.
+// Workspace of the native path: the reserved counters, then the partial
+// slots (units + waves).
 size_t native_workspace_bytes(int N, int Hq, int Hkv, int D) {
   const int W = persistent_waves();
   const int G = Hq / Hkv;
   const size_t slots = (size_t)N * Hkv + W;
-  const size_t fl = slots * G * (D + 2);
-  return fl * sizeof(float) + (size_t)(N + 2) * sizeof(int32_t) + 256;
+  return kWsReserved + slots * G * (D + 2) * sizeof(float);
 }
 
 int native_paged_decode(const void* q, const void* k_cache, const void* v_cache, const int32_t* block_tables,
                         int64_t table_stride, const int32_t* seq_rows, const int32_t* seq_lens,
                         int64_t num_blocks, void* out, int N, int Hq, int Hkv, int D, int block_size,
                         float scale, int dtype, void* workspace, size_t workspace_bytes, hipStream_t stream) {
-  if (N > kNativeMaxN) return MENTAT_EUNSUP;
+  if (N > kNativeMaxN || (long)N * Hkv > kMaxNativeUnits) return MENTAT_EUNSUP;
   if (block_size != 16 && block_size != 32 && block_size != 64) return MENTAT_EUNSUP;
   if (!block_tables || !seq_lens || table_stride <= 0 || num_blocks <= 0) return MENTAT_EINVAL;
   const size_t need = native_workspace_bytes(N, Hq, Hkv, D);
@@ -486,9 +485,9 @@ int native_paged_decode(const void* q, const void* k_cache, const void* v_cache,
   p.scale_log2 = scale * kLog2e;
   const int G = Hq / Hkv;
   const size_t slots = (size_t)N * Hkv + p.W;
-  p.ws_o = (float*)workspace;
+  p.ctr = (int32_t*)workspace;
+  p.ws_o = (float*)((char*)workspace + kWsReserved);
   p.ws_ml = p.ws_o + slots * G * D;
-  p.ws_meta = (int32_t*)(p.ws_ml + slots * G * 2);
   switch (dtype) {
     case MENTAT_BF16: return native_d<BF16>(D, G, p, stream);
     case MENTAT_F16: return native_d<F16>(D, G, p, stream);

@@ -540,7 +540,7 @@ using namespace mentat;
 extern "C" size_t mentat_tree_decode_workspace_bytes(int n_slots, int Hq, int Hkv, int D) {
   if (n_slots <= 0 || Hkv <= 0) return 0;
   const int G = Hq / Hkv;
-  return (size_t)n_slots * G * (D + 2) * sizeof(float);
+  return kWsReserved + (size_t)n_slots * G * (D + 2) * sizeof(float);
 }
 
 extern "C" int mentat_tree_decode(const void* q, const void* k_store, const void* v_store, const int32_t* block_tables,
@@ -560,7 +560,7 @@ extern "C" int mentat_tree_decode(const void* q, const void* k_store, const void
   p.q = q; p.k = k_store; p.v = v_store; p.tables = block_tables; p.table_stride = table_stride;
   p.num_blocks = num_blocks; p.items = items; p.n_shared = n_shared; p.n_solo = n_solo; p.members = members;
   const int G = Hq / Hkv;
-  p.ws_o = (float*)workspace;
+  p.ws_o = (float*)((char*)workspace + kWsReserved);
   p.ws_ml = p.ws_o + (size_t)n_slots * G * D;
   p.q_slot_off = q_slot_offsets; p.q_slots = q_slots; p.out = out;
   p.Nq = Nq; p.Hq = Hq; p.Hkv = Hkv; p.B = block_size; p.scale_log2 = scale * kLog2e;

@@ -179,3 +179,33 @@ def hf_top_p_keep(x: np.ndarray, temperature: float, top_p: float) -> np.ndarray
     keep = np.zeros(x.size, dtype=bool)
     keep[order[~remove]] = True
     return keep
+
+
+def reference_cpu_rows(logits, temperature: float, top_p: float, gate_threshold: float, seed: int = 0):
+    """The reference's per-row CPU path in torch, in the logits dtype: the
+    entropy gate of _step_leaf (compute_entropy at the gate temperature,
+    core/generator_utils.py:196-202, core/generator.py:342) and HF sampling
+    (TemperatureLogitsWarper + TopPLogitsWarper + multinomial,
+    transformers generation/logits_process.py:301-303, :527-540,
+    generation/utils.py:2923), one row at a time as the generator does.
+    Used as the timed CPU baseline. Returns (entropies, gate flags, ids)."""
+    import torch
+
+    g = torch.Generator().manual_seed(seed)
+    ents, gates, ids = [], [], []
+    for x in logits:
+        z = x / temperature
+        p = torch.softmax(z, dim=-1)
+        lp = torch.log_softmax(z, dim=-1)
+        t = p * lp
+        h = -torch.where(torch.isnan(t), torch.zeros_like(t), t).sum().item()
+        ents.append(h)
+        gates.append(h > gate_threshold)
+        s, order = torch.sort(z, descending=False)
+        cum = s.softmax(dim=-1).cumsum(dim=-1)
+        remove = cum <= (1 - top_p)
+        remove[-1:] = False
+        z2 = z.clone()
+        z2[order[remove]] = -float("inf")
+        ids.append(int(torch.multinomial(torch.softmax(z2.float(), dim=-1), 1, generator=g)))
+    return ents, gates, ids

@@ -31,7 +31,9 @@ def test_abi_version_and_pure_host_queries():
     # Pure host arithmetic: no device needed.
     assert lib.mentat_paged_decode_workspace_bytes(0, 0, 32, 8, 128, 16, 4096, 0) == 0
     nb = lib.mentat_paged_decode_workspace_bytes(0, 64, 32, 8, 128, 16, 4096, 256)
-    assert nb == 64 * 32 * 16 * (128 + 2) * 4
+    assert nb == 262144 + 64 * 32 * 16 * (128 + 2) * 4  # reserved counters + partials
+    assert lib.mentat_tree_decode_workspace_bytes(0, 32, 8, 128) == 0
+    assert lib.mentat_tree_decode_workspace_bytes(10, 32, 8, 128) == 262144 + 10 * 4 * 130 * 4
     c = lib.mentat_paged_decode_auto_chunk(64, 8, 16, 4096)
     assert c % 16 == 0 and 16 <= c <= 4096
     assert isinstance(lib.mentat_paged_decode, ctypes._CFuncPtr)

@@ -195,3 +195,39 @@ def test_llama3_8b_shapes_full_size(gpu, layout):
         vp = _to64(b.v_pool[pages]).reshape(-1, 8, 128)[: b.lens[i]]
         ref = sdpa_decode_f64(q64[i:i + 1], kp, vp, np.array([0, b.lens[i]]), b.scale)
         np.testing.assert_allclose(o[i], ref[0], atol=2e-2, rtol=1e-2, err_msg=f"seq {i}")
+
+
+def test_native_split_units_repeat_and_shared_workspace(gpu):
+    """The native kernel merges split units through arrival counters kept in the
+    workspace's reserved prefix. Repeated calls, interleaved with the other
+    entry points on the same workspace, must give identical results and leave
+    the counters zero."""
+    print("case native repeat + shared workspace", flush=True)
+    rng = np.random.default_rng(21)
+    lens = rng.integers(1, 3000, size=40).tolist()
+    b = paged_decode_batch(N=len(lens), Hq=32, Hkv=8, D=128, device=gpu, num_blocks=16384,
+                           lens=lens, seed=21, layout=LAYOUT_NATIVE)
+    r = paged_decode_batch(N=6, Hq=32, Hkv=8, D=128, device=gpu, num_blocks=512,
+                           lens=[900, 17, 2000, 5, 1200, 333], seed=22)
+
+    def native():
+        return ops.paged_decode(b.q, b.k_store, b.v_store, layout=LAYOUT_NATIVE, block_tables=b.block_tables,
+                                seq_lens=b.seq_lens, max_seqlen=b.max_seqlen, scale=b.scale)
+
+    first = native()
+    for _ in range(3):
+        ops.paged_decode(r.q, r.k_store, r.v_store, layout=LAYOUT_REFERENCE, block_tables=r.block_tables,
+                         seq_lens=r.seq_lens, max_seqlen=r.max_seqlen, chunk_tokens=16, scale=r.scale)
+        again = native()
+        torch.cuda.synchronize()
+        assert torch.equal(first, again)
+    ws = ops.workspace(gpu, 1)
+    assert int(ws[:262144].count_nonzero()) == 0
+    o = _to64(first)
+    q64 = _to64(b.q)
+    for i in range(0, len(lens), 3):
+        pages = torch.tensor(b.tables[i], dtype=torch.long, device=gpu)
+        kp = _to64(b.k_pool[pages]).reshape(-1, 8, 128)[: lens[i]]
+        vp = _to64(b.v_pool[pages]).reshape(-1, 8, 128)[: lens[i]]
+        ref = sdpa_decode_f64(q64[i:i + 1], kp, vp, np.array([0, lens[i]]), b.scale)
+        np.testing.assert_allclose(o[i], ref[0], atol=2e-2, rtol=1e-2, err_msg=f"seq {i}")

@@ -110,3 +110,26 @@ def test_pool_views_have_reference_shape():
         # writes through the view land in the storage of that layer only
         m.k_pools[1][3, 5, 2] = 7.0
         assert float(m.k_pools[1][3, 5, 2, 0]) == 7.0 and float(m.k_pools[0].abs().sum()) == 0.0
+
+
+def test_find_blocked_tokens_closed_forms():
+    from mentat_amd.core.generator_utils import _find_blocked_tokens
+
+    assert _find_blocked_tokens([], 3) == set()
+    assert _find_blocked_tokens([5], 3) == set()
+    # bigram: last token 1 occurred at 0 and 2, followed by 2 and 3
+    assert _find_blocked_tokens([1, 2, 1, 3, 1], 2) == {2, 3}
+    # trigram adds what followed "3 1"? "3 1" occurs only at the end -> nothing more
+    assert _find_blocked_tokens([1, 2, 1, 3, 1], 3) == {2, 3}
+    # "1 2" repeated: trigram blocks the 7 that followed the first "1 2"
+    assert _find_blocked_tokens([1, 2, 7, 1, 2], 3) == {7}
+    rng = random.Random(0)
+    for _ in range(50):  # brute force over every earlier window
+        ids = [rng.randint(0, 3) for _ in range(rng.randint(0, 12))]
+        mx = rng.randint(2, 4)
+        want = set()
+        for n in range(2, mx + 1):
+            for i in range(len(ids) - n + 1):
+                if len(ids) >= n and ids[i:i + n - 1] == ids[len(ids) - n + 1:]:
+                    want.add(ids[i + n - 1])
+        assert _find_blocked_tokens(ids, mx) == want
