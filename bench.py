@@ -16,6 +16,10 @@ Other workloads (their own JSON line, same fields):
                     of 32 leaves over 2048-token prompts (GB/s of unique bytes)
   --workload rows   fused entropy gate + temperature/top-p sampling over
                     [256, 151936] bf16 logits (GB/s of logits bytes)
+  --workload e2e    end-to-end rollout: random-init Llama-3-8B bf16, 16 prompts
+                    of 256 ids, 512 new tokens, absolute gate 2.5 nats, up to 8
+                    branches per prompt, all prompts continuously batched
+                    (branch-decode tokens/s)
 
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload decode|tree|rows]
 """
@@ -335,12 +339,80 @@ def run_rows(args, dev) -> dict:
     return line
 
 
+class _IdTokenizer:
+    """Prompts are token ids; decoding joins ids (the rollout never needs text)."""
+
+    def __init__(self, eos: int):
+        self.eos_token_id = eos
+
+    def decode(self, ids, skip_special_tokens=True):
+        return " ".join(str(i) for i in ids)
+
+
+def run_e2e(args, dev) -> dict:
+    import numpy as np
+    import torch
+    from transformers import LlamaConfig, LlamaForCausalLM
+
+    from mentat_amd.core.batch_generator import MentatBatchGenerator
+
+    print("bench: building random-init Llama-3-8B (bf16)", file=sys.stderr, flush=True)
+    cfg = LlamaConfig(hidden_size=4096, num_hidden_layers=32, num_attention_heads=32, num_key_value_heads=8,
+                      head_dim=128, intermediate_size=14336, vocab_size=128256, max_position_embeddings=8192,
+                      rms_norm_eps=1e-5, initializer_range=0.02, tie_word_embeddings=False)
+    cfg.rope_parameters = {"rope_theta": 500000.0, "rope_type": "default"}
+    torch.manual_seed(0)
+    prev = torch.get_default_dtype()
+    torch.set_default_dtype(torch.bfloat16)
+    try:
+        with torch.device(dev):
+            model = LlamaForCausalLM(cfg)
+    finally:
+        torch.set_default_dtype(prev)
+    model.eval()
+    n_prompts, prompt_len, new_tokens = 16, 256, args.e2e_new_tokens
+    prompts = [np.random.default_rng(s).integers(0, cfg.vocab_size, prompt_len).tolist() for s in range(n_prompts)]
+    knobs = dict(gate="absolute", entropy_threshold=2.5, max_active_branches=8, branching_factor=3,
+                 block_size=16, max_blocks=196608)
+    with torch.no_grad():
+        print("bench: warmup rollout", file=sys.stderr, flush=True)
+        warm = MentatBatchGenerator(model, _IdTokenizer(128001), max_new_tokens=8, **knobs)
+        warm.generate_batch(prompts[:4])
+        del warm
+        torch.cuda.empty_cache()
+        print("bench: timed rollout", file=sys.stderr, flush=True)
+        gen = MentatBatchGenerator(model, _IdTokenizer(128001), max_new_tokens=new_tokens, **knobs)
+        results = gen.generate_batch(prompts)
+    d = gen.get_batch_diagnostics()
+    steps = d["decode_steps"]
+    ms = d["decode_time_s"] * 1e3 / max(steps, 1)
+    wbytes = sum(p.numel() * p.element_size() for p in model.parameters())
+    config = {
+        "workload": "end-to-end MENTAT rollout, random-init Llama-3-8B bf16",
+        "prompts": n_prompts, "prompt_tokens": prompt_len, "new_tokens": new_tokens,
+        "gate": "absolute 2.5 nats", "max_branches_per_prompt": 8, "branching_factor": 3,
+        "batching": "all prompts' live leaves in one decode batch per step (continuous batching)",
+        "decode_steps": steps, "decode_tokens": d["decode_tokens_total"], "max_live_leaves": d["max_live_leaves"],
+        "results": sum(len(r) for r in results), "kv_blocks_peak": d["kv_blocks_peak"],
+        "weight_bytes": wbytes,
+    }
+    line = _line(args, 0.0, ms, config, None, None)
+    line.update({"metric": METRIC, "value": round(d["decode_throughput_tps"], 1), "unit": "tokens/s"})
+    # per-step HBM floor: the weights once per step
+    line["roofline"] = {"bound": "hbm", "achieved": round(wbytes / (ms * 1e-3) / 1e9, 1), "peak": PEAK_HBM_GBS,
+                        "unit": "GB/s", "frac": round(wbytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+                        "traffic": None, "note": "achieved = weight bytes per decode step / step time"}
+    line["data"] = "synthetic (random-init weights, seed 0; prompts of uniform random ids, seeds 0-15)"
+    return line
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--workload", choices=("decode", "tree", "rows"), default="decode")
+    ap.add_argument("--workload", choices=("decode", "tree", "rows", "e2e"), default="decode")
+    ap.add_argument("--e2e-new-tokens", type=int, default=512)
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="minimum host time spent on the CPU baseline")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -357,7 +429,7 @@ def main() -> int:
 
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
-    run = {"decode": run_decode, "tree": run_tree, "rows": run_rows}[args.workload]
+    run = {"decode": run_decode, "tree": run_tree, "rows": run_rows, "e2e": run_e2e}[args.workload]
     print(json.dumps(run(args, dev)), flush=True)
     return 0
 

@@ -1,0 +1,184 @@
+"""Cross-prompt continuous batching of MENTAT rollouts.
+
+The reference rolls prompts out one after another (mentat_rollout.py:256-259;
+the server serialises requests, mentat_server.py:351), so each decode step is
+one prompt's handful of branches. Here up to ``max_trees`` prompt trees are
+live at once over ONE paged KV cache: every decode step runs all live leaves
+of all trees through one batched forward (PagedModelWrapper.decode_batch_tensor)
+and one fused row-kernel call, and a finished tree's slot is refilled from the
+queue (prefill + its step-0 decision) before the next step.
+
+Each tree keeps the reference's per-prompt rules exactly (core/generator.py:
+125-374): its own step counter (soft-explore warm-up, max_new_tokens), its own
+num_active frozen at the start of the step (headroom M - num_active, the
+relative gate's utilisation), its own EMAs, DFS batch order within the tree and
+its own semantic-similarity prune. Given the same logits, a prompt's tree is
+the one MentatGenerator.generate would build for it alone; only physical block
+ids differ (one allocator serves every tree).
+
+Metric (A12's definition over the whole batch): branch-decode tokens/s =
+sum over decode steps of the live leaves / decode wall time (prefill and the
+step-0 decisions of the first admitted prompts excluded).
+"""
+from __future__ import annotations
+
+import math
+import time
+from dataclasses import dataclass, field
+
+import torch
+
+from .generator import MentatGenerator
+from .generator_utils import PrefixTree, TreeNode
+
+__all__ = ["MentatBatchGenerator"]
+
+
+@dataclass
+class _TreeRun:
+    index: int                  # prompt index
+    tree: PrefixTree
+    step: int = 1               # next decode step of this tree
+    prefill_tokens: int = 0
+    entropy_trace: list = field(default_factory=list)
+    branch_points: list = field(default_factory=list)
+    diversity_pruning_events: list = field(default_factory=list)
+    active_branch_trace: list = field(default_factory=list)
+    decode_tokens: int = 0
+
+
+class MentatBatchGenerator(MentatGenerator):
+    """MentatGenerator over many prompts at once (same constructor)."""
+
+    def generate_batch(self, prompts: list, max_trees: int | None = None) -> list[list[dict]]:
+        """Roll out every prompt (strings through the tokenizer, or lists of ids);
+        returns each prompt's results, as MentatGenerator.generate does, in prompt order."""
+        dev = self.wrapper.device
+        on_gpu = dev.type == "cuda"
+        if on_gpu:
+            torch.cuda.reset_peak_memory_stats(dev)
+        max_trees = len(prompts) if max_trees is None else max(1, int(max_trees))
+        queue = list(range(len(prompts)))
+        live: list[_TreeRun] = []
+        done: dict[int, list[dict]] = {}
+        self.runs: dict[int, _TreeRun] = {}
+        self.batch_trace: list[int] = []
+        self._total_tokens_decoded = 0
+        self._prefill_tokens = 0
+        prefill_s = 0.0
+
+        def admit():
+            nonlocal prefill_s
+            while queue and len(live) < max_trees:
+                idx = queue.pop(0)
+                t0 = time.perf_counter()
+                run = self._start_tree(idx, prompts[idx])
+                if on_gpu:
+                    torch.cuda.synchronize(dev)
+                prefill_s += time.perf_counter() - t0
+                self.runs[idx] = run
+                live.append(run)
+
+        admit()
+        t_start = time.perf_counter()
+        prefill_before = prefill_s
+        while live:
+            # retire finished trees, refill their slots
+            for run in list(live):
+                if run.step >= self.max_new_tokens or not run.tree.get_active_leaves():
+                    done[run.index] = self._finish_tree(run)
+                    live.remove(run)
+            admit()
+            if not live:
+                break
+            batch, trees, steps, nacts, logs = [], [], [], [], []
+            for run in live:
+                leaves = run.tree.get_active_leaves()
+                run.active_branch_trace.append(len(leaves))
+                run.decode_tokens += len(leaves)
+                batch += leaves
+                trees += [run.tree] * len(leaves)
+                steps += [run.step] * len(leaves)
+                nacts += [len(leaves)] * len(leaves)
+                logs += [run] * len(leaves)
+            self.batch_trace.append(len(batch))
+            logits, hidden = self.wrapper.decode_batch_tensor([l.token_ids[-1] for l in batch],
+                                                              [l.seq_id for l in batch])
+            self._total_tokens_decoded += len(batch)
+            self._update_semantic_vectors(batch, hidden)
+            self._decide_rows(batch, logits, trees, steps, nacts, logs)
+            for run in live:
+                self._prune_similar(run.tree, run.step, log=run)
+                if self.step_hook is not None:
+                    self.step_hook(run.step, run.tree)
+                run.step += 1
+        if on_gpu:
+            torch.cuda.synchronize(dev)
+        # prefill of prompts admitted after the start is not decode time
+        self._decode_time_s = time.perf_counter() - t_start - (prefill_s - prefill_before)
+        self._prefill_time_s = prefill_s
+        if on_gpu:
+            self._peak_vram_bytes = torch.cuda.max_memory_allocated(dev)
+        return [done[i] for i in range(len(prompts))]
+
+    # ------------------------------------------------------------------
+    def _start_tree(self, idx: int, prompt) -> _TreeRun:
+        dev = self.wrapper.device
+        if isinstance(prompt, str):
+            input_ids = self.tokenizer(prompt, return_tensors="pt")["input_ids"].to(dev)
+        else:
+            input_ids = torch.tensor([list(prompt)], dtype=torch.long, device=dev)
+        seq_id = self.kv_cache_mgr.allocate_sequence()
+        logits = self.wrapper.prefill(input_ids, seq_id)
+        tree = PrefixTree(self.kv_cache_mgr)
+        first = TreeNode(node_id=tree.new_id(), token_ids=[], seq_id=seq_id, parent=tree.root,
+                         cumulative_log_prob=0.0, depth=0, is_active=True)
+        tree.root.children[0] = first
+        run = _TreeRun(index=idx, tree=tree, prefill_tokens=int(input_ids.shape[-1]))
+        self._prefill_tokens += run.prefill_tokens
+        self._decide_rows([first], logits.unsqueeze(0), [tree], [0], [1], [run])
+        return run
+
+    def _finish_tree(self, run: _TreeRun) -> list[dict]:
+        tree = run.tree
+        results = []
+        for node in tree.get_complete_sequences() + tree.get_active_leaves():
+            tids = node.get_full_sequence()
+            length = max(len(tids), 1)
+            results.append({
+                "token_ids": tids,
+                "text": self.tokenizer.decode(tids, skip_special_tokens=True),
+                "log_prob": node.cumulative_log_prob,
+                "norm_prob": math.exp(node.cumulative_log_prob / length),
+            })
+        self._free_walk(tree.root)
+        results.sort(key=lambda r: r["norm_prob"], reverse=True)
+        return results
+
+    def get_batch_diagnostics(self) -> dict:
+        """Whole-batch metric plus each prompt's traces (the reference's per-prompt keys)."""
+        tps = self._total_tokens_decoded / self._decode_time_s if self._decode_time_s > 0 else 0.0
+        kv = self.kv_cache_mgr.get_stats()
+        return {
+            "decode_tokens_total": self._total_tokens_decoded,
+            "decode_time_s": round(self._decode_time_s, 4),
+            "decode_throughput_tps": round(tps, 2),
+            "decode_steps": len(self.batch_trace),
+            "max_live_leaves": max(self.batch_trace) if self.batch_trace else 0,
+            "prefill_tokens": self._prefill_tokens,
+            "prefill_time_s": round(self._prefill_time_s, 4),
+            "peak_vram_bytes": self._peak_vram_bytes,
+            "kv_blocks_peak": kv["blocks_peak"],
+            "peak_kv_cache_bytes_true": kv["peak_kv_cache_bytes_true"],
+            "prompts": {
+                i: {
+                    "num_branch_points": len(r.branch_points),
+                    "branch_points": r.branch_points,
+                    "entropy_trace": r.entropy_trace,
+                    "active_branch_trace": r.active_branch_trace,
+                    "diversity_pruning_events": r.diversity_pruning_events,
+                    "decode_tokens": r.decode_tokens,
+                }
+                for i, r in self.runs.items()
+            },
+        }

@@ -197,6 +197,14 @@ class MentatGenerator:
     def _decide(self, tree: PrefixTree, leaves: list[TreeNode], logits: torch.Tensor, step: int,
                 num_active: int) -> None:
         """Gate + branch/extend for every leaf of the batch (reference _step_leaf, :333-374)."""
+        n = len(leaves)
+        self._decide_rows(leaves, logits, [tree] * n, [step] * n, [num_active] * n, [self] * n)
+
+    def _decide_rows(self, leaves: list[TreeNode], logits: torch.Tensor, trees: list, steps: list,
+                     num_actives: list, logs: list) -> None:
+        """_decide over a batch whose leaves may belong to different trees: leaf i
+        follows the rules with its own tree's step, frozen num_active, and appends
+        to logs[i].entropy_trace / .branch_points."""
         off, ids = self._penalty_csr(leaves)
         st = ops.row_stats(
             logits.contiguous(), temperature=self.temperature, penalty=self.rep_penalty,
@@ -211,8 +219,9 @@ class MentatGenerator:
         for i, leaf in enumerate(leaves):
             if not leaf.is_active:
                 continue
+            tree, step, num_active, log = trees[i], steps[i], num_actives[i], logs[i]
             H = float(rec_cpu[i, 0])
-            self.entropy_trace.append((step, leaf.node_id, H))
+            log.entropy_trace.append((step, leaf.node_id, H))
             if leaf.entropy_ema is None:
                 leaf.entropy_ema = H
             else:
@@ -228,7 +237,7 @@ class MentatGenerator:
             top_lps = [float(x) for x in rec_cpu[i, 2:2 + self.K]]
             if open_gate and headroom >= self.K:
                 children = tree.branch_leaf(leaf, top_ids, top_lps)
-                self.branch_points.append((step, float(rec_cpu[i, 1]), len(children)))
+                log.branch_points.append((step, float(rec_cpu[i, 1]), len(children)))
                 for child in children:
                     child.creation_step = step
                     self._handle_eos(tree, child)
@@ -269,7 +278,8 @@ class MentatGenerator:
             else:
                 leaf.semantic_vector.mul_(1.0 - a).add_(h, alpha=a)
 
-    def _prune_similar(self, tree: PrefixTree, step: int) -> None:
+    def _prune_similar(self, tree: PrefixTree, step: int, log=None) -> None:
+        log = self if log is None else log
         leaves = tree.get_active_leaves()
         if len(leaves) <= 1:
             return
@@ -305,7 +315,7 @@ class MentatGenerator:
                 tree.prune_branch(leaf)
                 pruned += 1
         if pruned:
-            self.diversity_pruning_events.append((step, pruned))
+            log.diversity_pruning_events.append((step, pruned))
 
     # ------------------------------------------------------------------
     def get_diagnostics(self) -> dict:

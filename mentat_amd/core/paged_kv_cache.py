@@ -7,12 +7,18 @@ tables and counters per sequence (:79-96), fork/free (:152-176) and the lazy
 copy-on-write rules of append (:178-284).
 
 Device side (new):
-  * pools live in one allocation per K/V. 16-bit pools with block_size % 16 == 0
-    use the native layout read by the MFMA decode kernel (K [blk][Hkv][B][D],
+  * one K store and one V store of ``max_blocks`` pages serve every layer. The
+    reference gives each layer its own ``max_blocks`` pool (:124-138), but its
+    single allocator hands every block id to exactly one (sequence, layer) —
+    fork shares an id within its layer, copy-on-write takes a fresh one — so a
+    page id is never live in two layers and one store holds them all, with
+    1/num_layers of the memory. 16-bit pools with block_size % 16 == 0 use the
+    native layout read by the MFMA decode kernel (K [blk][Hkv][B][D],
     V [blk][Hkv][D][B]); other pools keep the reference layout. ``k_pools[l]`` /
-    ``v_pools[l]`` are always ``[max_blocks, block_size, Hkv, D]``-shaped views
-    (permuted views for the native layout), so ``k_pools[l][blk, slot]`` means
-    what it means in the reference.
+    ``v_pools[l]`` are ``[max_blocks, block_size, Hkv, D]``-shaped views of the
+    shared stores (permuted views for the native layout), so
+    ``k_pools[l][blk, slot]`` means what it means in the reference for every
+    block id that layer ``l`` owns.
   * every live sequence owns a row of int32 device block tables
     ``[num_layers, rows, pages]`` and lengths ``[num_layers, rows]``. The append
     kernel writes the table entry and length of each token it stores and
@@ -171,17 +177,18 @@ class PagedKVCacheManager:
         L, nb, B, H, D = num_layers, max_blocks, block_size, num_key_value_heads, head_dim
         native = dtype in (torch.bfloat16, torch.float16) and B % 16 == 0 and D % 32 == 0
         self.layout = LAYOUT_NATIVE if native else LAYOUT_REFERENCE
-        # Pools are zero-initialised, as in the reference (:124-138).
+        # Pools are zero-initialised, as in the reference (:124-138); one store per
+        # K/V for all layers (see the module docstring).
         if native:
-            self._k_store = torch.zeros(L, nb, H, B, D, device=self.device, dtype=dtype)
-            self._v_store = torch.zeros(L, nb, H, D, B, device=self.device, dtype=dtype)
-            self.k_pools = [self._k_store[l].permute(0, 2, 1, 3) for l in range(L)]
-            self.v_pools = [self._v_store[l].permute(0, 3, 1, 2) for l in range(L)]
+            self._k_store = torch.zeros(nb, H, B, D, device=self.device, dtype=dtype)
+            self._v_store = torch.zeros(nb, H, D, B, device=self.device, dtype=dtype)
+            self.k_pools = [self._k_store.permute(0, 2, 1, 3)] * L
+            self.v_pools = [self._v_store.permute(0, 3, 1, 2)] * L
         else:
-            self._k_store = torch.zeros(L, nb, B, H, D, device=self.device, dtype=dtype)
-            self._v_store = torch.zeros(L, nb, B, H, D, device=self.device, dtype=dtype)
-            self.k_pools = [self._k_store[l] for l in range(L)]
-            self.v_pools = [self._v_store[l] for l in range(L)]
+            self._k_store = torch.zeros(nb, B, H, D, device=self.device, dtype=dtype)
+            self._v_store = torch.zeros(nb, B, H, D, device=self.device, dtype=dtype)
+            self.k_pools = [self._k_store] * L
+            self.v_pools = [self._v_store] * L
 
         # Device block tables / lengths, one row per live sequence (grown on demand).
         self._rows_cap = 64
@@ -347,7 +354,7 @@ class PagedKVCacheManager:
         k = k.to(self.dtype).contiguous()
         v = v.to(self.dtype).contiguous()
         ops.kv_append(
-            k, v, self._k_store[layer_idx], self._v_store[layer_idx], plan_t,
+            k, v, self._k_store, self._v_store, plan_t,
             block_size=self.block_size, layout=self.layout,
             block_tables=self._tables[layer_idx], seq_lens=self._lens[layer_idx],
         )
@@ -399,8 +406,8 @@ class PagedKVCacheManager:
         rows = self._rows_tensor(key) if seq_ids else torch.zeros(0, dtype=torch.int32, device=self.device)
         common = dict(tables=self._tables[layer_idx], lens=self._lens[layer_idx], rows=rows,
                       block_size=self.block_size, layout=self.layout, max_seqlen=max_len)
-        kv = PagedKVView(store=self._k_store[layer_idx], **common)
-        vv = PagedKVView(store=self._v_store[layer_idx], **common)
+        kv = PagedKVView(store=self._k_store, **common)
+        vv = PagedKVView(store=self._v_store, **common)
         return kv, vv, cu, max_len
 
     def gather_packed_kv(self, seq_ids: list[int], layer_idx: int):
@@ -495,7 +502,8 @@ class PagedKVCacheManager:
             "blocks_peak": self.allocator.peak_used,
             "utilization": self.allocator.num_used / self.max_blocks,
             "peak_utilization": self.allocator.peak_used / self.max_blocks,
-            "pool_memory_bytes": bytes_per_block * self.max_blocks,
+            "pool_memory_bytes": bytes_per_block * self.max_blocks,  # reference formula (L pools)
+            "pool_memory_bytes_true": true_bytes_per_block * self.max_blocks,  # the shared stores
             "peak_kv_cache_bytes": bytes_per_block * self.allocator.peak_used,
             # Each block id holds one layer's K and V page: the bytes actually in use.
             "peak_kv_cache_bytes_true": true_bytes_per_block * self.allocator.peak_used,

@@ -322,6 +322,6 @@ def prefix_tree_batch(*, n_trees: int = 4, prefix: int = 2048, leaves: int = 32,
         tables=[list(st.page_table[0]) for st in states],
         rows=[st.row for st in states],
         block_tables=mgr._tables[0], seq_lens=mgr._lens[0],
-        k_store=mgr._k_store[0], v_store=mgr._v_store[0],
+        k_store=mgr._k_store, v_store=mgr._v_store,
         block_size=block_size, scale=1.0 / float(np.sqrt(D)),
     )

@@ -107,9 +107,42 @@ def test_pool_views_have_reference_shape():
         assert tuple(m.k_pools[1].shape) == (8, 16, 4, 64)
         assert tuple(m.v_pools[0].shape) == (8, 16, 4, 64)
         assert (m.layout == 1) == layout_native
-        # writes through the view land in the storage of that layer only
+        # one store for all layers: a block id is owned by one layer at a time,
+        # so every layer's view of a page is the same memory
         m.k_pools[1][3, 5, 2] = 7.0
-        assert float(m.k_pools[1][3, 5, 2, 0]) == 7.0 and float(m.k_pools[0].abs().sum()) == 0.0
+        assert float(m.k_pools[1][3, 5, 2, 0]) == 7.0 and float(m.k_pools[0][3, 5, 2, 0]) == 7.0
+        assert float(m.k_pools[0].abs().sum()) == 7.0 * 64
+        st = m.get_stats()
+        assert st["pool_memory_bytes_true"] * 2 == st["pool_memory_bytes"]
+
+
+def test_block_ids_are_owned_by_one_layer():
+    """The invariant that lets all layers share one store: at every point of a
+    random trace of allocate / fork / append / free, no block id is in the
+    tables of two different layers."""
+    rng = random.Random(5)
+    L, nb, B = 4, 4096, 8
+    m = PagedKVCacheManager(L, 2, 16, max_blocks=nb, block_size=B, device="cpu", dtype=torch.float32)
+    for _ in range(300):
+        live = list(m._sequences)
+        op = rng.random()
+        if not live or op < 0.15:
+            sid = m.allocate_sequence()
+            for layer in range(L):
+                m.plan_append(sid, layer, rng.randint(0, 20))
+        elif op < 0.35:
+            m.fork_sequence(rng.choice(live))
+        elif op < 0.5 and len(live) > 1:
+            m.free_sequence(rng.choice(live))
+        else:
+            ids = rng.sample(live, rng.randint(1, len(live)))
+            for layer in range(L):
+                m.plan_append_batched(ids, layer)
+        owner = {}
+        for st in m._sequences.values():
+            for layer, table in enumerate(st.page_table):
+                for b in table:
+                    assert owner.setdefault(b, layer) == layer
 
 
 def test_find_blocked_tokens_closed_forms():
