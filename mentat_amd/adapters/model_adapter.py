@@ -127,7 +127,11 @@ class ModelAdapter(abc.ABC):
         """(1, S, hidden) -> attn_output (1, S, hidden), k_new / v_new (S, Hkv, D) post-RoPE."""
         _, seq_len, _ = hidden_states.size()
         q, k, v = self.project_qkv(attn, hidden_states)
-        pos = torch.arange(seq_len, device=q.device, dtype=torch.long).unsqueeze(0)
+        pp = getattr(self, "_prefill_pos", None)
+        if pp is None or pp.shape[1] != seq_len or pp.device != q.device:
+            pp = torch.arange(seq_len, device=q.device, dtype=torch.long).unsqueeze(0)
+            self._prefill_pos = pp
+        pos = pp
         q, k = self.apply_rope(attn, q, k, pos, v_for_shape=v)
         o = self.flash_prefill(q, k, v, window_size)
         o = attn.o_proj(o.reshape(1, seq_len, -1))
@@ -200,8 +204,17 @@ class _HFDecoderAdapter(ModelAdapter):
         return layer.post_attention_layernorm(hidden)
 
     def _build_cos_sin(self, position_ids, ref):
+        # Every layer of a decode step rotates at the same positions (the same
+        # tensor object from _positions): compute cos/sin once per step. The
+        # cache holds the position tensor itself, so identity is reliable.
+        c = getattr(self, "_cs_cache", None)
+        if (c is not None and c[0] is position_ids and c[1] == position_ids._version
+                and c[2] == ref.dtype and c[3] == ref.device):
+            return c[4], c[5]
         cos, sin = self._rotary_emb(ref, position_ids)
-        return cos.unsqueeze(2), sin.unsqueeze(2)
+        cos, sin = cos.unsqueeze(2), sin.unsqueeze(2)
+        self._cs_cache = (position_ids, position_ids._version, ref.dtype, ref.device, cos, sin)
+        return cos, sin
 
     @staticmethod
     def _apply_cos_sin(t, cos, sin):

@@ -107,8 +107,8 @@ class MentatBatchGenerator(MentatGenerator):
             self._total_tokens_decoded += len(batch)
             self._update_semantic_vectors(batch, hidden)
             self._decide_rows(batch, logits, trees, steps, nacts, logs)
+            self._prune_runs(live)
             for run in live:
-                self._prune_similar(run.tree, run.step, log=run)
                 if self.step_hook is not None:
                     self.step_hook(run.step, run.tree)
                 run.step += 1
@@ -122,6 +122,33 @@ class MentatBatchGenerator(MentatGenerator):
         return [done[i] for i in range(len(prompts))]
 
     # ------------------------------------------------------------------
+    def _prune_runs(self, runs: list) -> None:
+        """Every tree's semantic-similarity prune (the rule of _prune_similar, per
+        tree) from one similarity matrix over all trees' eligible leaves: pairs
+        are kept only within a tree, so each tree sees exactly its own pairs, in
+        its own row-major order."""
+        all_sv, groups, per = [], [], []
+        for gi, run in enumerate(runs):
+            leaves = run.tree.get_active_leaves()
+            sv = []
+            if len(leaves) > 1:
+                sv = [l for l in leaves if l.semantic_vector is not None
+                      and run.step - l.creation_step >= self.min_steps_before_prune]
+            if len(sv) <= 1:
+                sv = []
+            per.append((run, len(all_sv), sv))
+            all_sv += sv
+            groups += [gi] * len(sv)
+        if len(all_sv) <= 1:
+            return
+        by_group: dict = {}
+        for i, j in self._similar_pairs(all_sv, groups):
+            by_group.setdefault(groups[i], []).append((i, j))
+        for gi, (run, base, sv) in enumerate(per):
+            pairs = by_group.get(gi)
+            if pairs:
+                self._apply_prune(run.tree, sv, [(i - base, j - base) for i, j in pairs], run.step, run)
+
     def _start_tree(self, idx: int, prompt) -> _TreeRun:
         dev = self.wrapper.device
         if isinstance(prompt, str):

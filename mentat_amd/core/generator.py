@@ -288,16 +288,11 @@ class MentatGenerator:
         M = len(sv_leaves)
         if M <= 1:
             return
-        sv = torch.stack([l.semantic_vector for l in sv_leaves], dim=0)
-        normed = F.normalize(sv, p=2, dim=1)
-        sim = torch.mm(normed, normed.t().contiguous())
-        mask = torch.triu(torch.ones(M, M, device=sim.device, dtype=torch.bool), diagonal=1)
-        for i in range(M):
-            for j in range(i + 1, M):
-                if sv_leaves[i].parent is not None and sv_leaves[i].parent is sv_leaves[j].parent:
-                    mask[i, j] = False
-        sim = sim * mask
-        pairs = (sim > self.semantic_similarity_threshold).nonzero(as_tuple=False).tolist()
+        pairs = self._similar_pairs(sv_leaves, [0] * M)
+        self._apply_prune(tree, sv_leaves, pairs, step, log)
+
+    def _apply_prune(self, tree: PrefixTree, sv_leaves: list[TreeNode], pairs: list, step: int, log) -> None:
+        """Greedy prune over the similar pairs in row-major order (reference :462-497)."""
         if not pairs:
             return
         to_prune: set[int] = set()
@@ -316,6 +311,23 @@ class MentatGenerator:
                 pruned += 1
         if pruned:
             log.diversity_pruning_events.append((step, pruned))
+
+    def _similar_pairs(self, sv_leaves: list[TreeNode], groups: list) -> list:
+        """(i, j), i < j, row-major: leaves of the same group (tree) whose semantic
+        vectors have cosine similarity above the threshold and that are not
+        siblings (reference :447-460; the mask is built on the host in one go)."""
+        M = len(sv_leaves)
+        sv = torch.stack([l.semantic_vector for l in sv_leaves], dim=0)
+        normed = F.normalize(sv, p=2, dim=1)
+        sim = torch.mm(normed, normed.t().contiguous())
+        par = np.array([id(l.parent) if l.parent is not None else -1 - i for i, l in enumerate(sv_leaves)])
+        grp = np.asarray(groups)
+        keep = np.triu(np.ones((M, M), dtype=bool), k=1)
+        keep &= par[:, None] != par[None, :]
+        keep &= grp[:, None] == grp[None, :]
+        mask = torch.from_numpy(keep).to(sim.device)
+        sim = sim * mask
+        return (sim > self.semantic_similarity_threshold).nonzero(as_tuple=False).tolist()
 
     # ------------------------------------------------------------------
     def get_diagnostics(self) -> dict:

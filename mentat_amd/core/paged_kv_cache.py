@@ -317,32 +317,36 @@ class PagedKVCacheManager:
         batch order): returns the int32 [7, N] plan."""
         B = self.block_size
         alloc = self.allocator
-        n = len(seq_ids)
-        plan = np.empty((7, n), dtype=np.int32)
-        for i, sid in enumerate(seq_ids):
-            seq = self._sequences[sid]
-            table = seq.page_table[layer_idx]
-            if not table or seq.tokens_in_last_block[layer_idx] == B:
+        rc = alloc.refcounts
+        seqs = self._sequences
+        L = layer_idx
+        dst, slots, cows, rows, pages, lens = [], [], [], [], [], []
+        for sid in seq_ids:
+            seq = seqs[sid]
+            table = seq.page_table[L]
+            tilb = seq.tokens_in_last_block
+            if not table or tilb[L] == B:
                 table.append(alloc.alloc())
-                seq.tokens_in_last_block[layer_idx] = 0
+                tilb[L] = 0
             tail = table[-1]
             cow = -1
-            if alloc.is_shared(tail):
+            if rc[tail] > 1:  # shared tail: copy-on-write (reference :258-265)
                 new_blk = alloc.alloc()
                 alloc.release(tail)
                 table[-1] = new_blk
                 cow, tail = tail, new_blk
-            slot = seq.tokens_in_last_block[layer_idx]
-            seq.tokens_in_last_block[layer_idx] = slot + 1
-            seq.num_tokens[layer_idx] += 1
-            plan[0, i] = tail
-            plan[1, i] = slot
-            plan[2, i] = cow
-            plan[3, i] = seq.row
-            plan[4, i] = len(table) - 1
-            plan[5, i] = seq.num_tokens[layer_idx]
-            plan[6, i] = i
-        return plan
+            slot = tilb[L]
+            tilb[L] = slot + 1
+            nt = seq.num_tokens
+            nt[L] += 1
+            dst.append(tail)
+            slots.append(slot)
+            cows.append(cow)
+            rows.append(seq.row)
+            pages.append(len(table) - 1)
+            lens.append(nt[L])
+        return np.array([dst, slots, cows, rows, pages, lens, list(range(len(seq_ids)))],
+                        dtype=np.int32).reshape(7, len(seq_ids))
 
     def _launch_append(self, layer_idx: int, k: torch.Tensor, v: torch.Tensor, plan: np.ndarray) -> None:
         if plan.shape[1] == 0:
