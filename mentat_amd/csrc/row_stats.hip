@@ -2,8 +2,12 @@
 // temperature + top-p sampling over the full vocabulary (gfx950).
 //
 // One 1024-thread workgroup per logits row. Every pass streams the row with
-// 16-byte loads in the order element = (chunk*1024 + thread)*EPV + e; the first
-// pass reads HBM, later passes are served from the L2 / MALL caches.
+// 16-byte loads in the order element = (chunk*1024 + thread)*EPV + e, eight
+// loads in flight per thread. Passes: maxima; entropy sums + the first radix
+// level of the sampler's masses; top-K (K passes, only when asked); the
+// sampler's deeper radix levels (elements of one bin only), the last one also
+// counting the chosen key's tokens per chunk, so the final index search reads
+// one chunk.
 //
 // Per row (reference semantics, cited):
 //   H_T      entropy of softmax(x / T) of the raw logits, in nats
@@ -155,12 +159,12 @@ struct RowShared {
   uint64_t u[kRowWaves];
   uint64_t hist0[kHistBins];  // first radix level (shared by both selections)
   uint64_t hist1[kHistBins];  // deeper levels
-  uint64_t part[kRowThreads];  // per-thread partial sums for the bin scans
   uint32_t sel[4];
   uint64_t sel64[4];
   float bk[kRowWaves];
   int32_t bi[kRowWaves];
   uint32_t chunk_tot[64];
+  uint32_t cc[64 * 16];  // per-chunk counts of the last radix level's values (<= 16 of them)
   int32_t scan[kRowThreads];
 };
 
@@ -213,6 +217,33 @@ __device__ __forceinline__ uint64_t block_sum_u64(uint64_t v, RowShared& sh) {
   return a;
 }
 
+// Exclusive prefix sum over the threads (thread order) and the total: a
+// wave-level scan, the wave totals through LDS, two barriers.
+__device__ __forceinline__ uint64_t shfl_up_u64(uint64_t v, int o) {
+  const uint32_t lo = __shfl_up((uint32_t)v, o), hi = __shfl_up((uint32_t)(v >> 32), o);
+  return ((uint64_t)hi << 32) | lo;
+}
+__device__ __forceinline__ uint64_t block_excl_scan_u64(uint64_t v, uint64_t& total, RowShared& sh) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  uint64_t inc = v;
+_Pragma("clang loop unroll(full)")
+  for (int o = 1; o < 64; o <<= 1) {
+    const uint64_t t = shfl_up_u64(inc, o);
+    if (lane >= o) inc += t;
+  }
+  __syncthreads();
+  if (lane == 63) sh.u[wave] = inc;
+  __syncthreads();
+  uint64_t base = 0, tot = 0;
+  for (int w = 0; w < kRowWaves; ++w) {
+    const uint64_t t = sh.u[w];
+    base += w < wave ? t : 0;
+    tot += t;
+  }
+  total = tot;
+  return base + inc - v;
+}
+
 // (key, idx) ordering for top-K: larger key first, then lower index.
 __device__ __forceinline__ bool tk_better(float ka, int ia, float kb, int ib) {
   return ka > kb || (ka == kb && ia < ib);
@@ -234,27 +265,59 @@ _Pragma("clang loop unroll(full)")
   }
 }
 
-// Stream the row in steps of four chunks (four 16-byte loads in flight per
-// thread); the body sees `c` (chunk) and `x` (its EPV elements). Expanded in
-// place so that accumulators stay in registers.
-#define ROW_FOR_GROUPS(...)                                              \
-  for (int c0_ = 0; c0_ < nchunks; c0_ += 4) {                           \
-    float xg_[4][EPV];                                                   \
-    _Pragma("clang loop unroll(full)") for (int u_ = 0; u_ < 4; ++u_)                     \
-      if (c0_ + u_ < nchunks) load_group(c0_ + u_, xg_[u_]);             \
-    _Pragma("clang loop unroll(full)") for (int u_ = 0; u_ < 4; ++u_) {                   \
-      if (c0_ + u_ < nchunks) {                                          \
-        const int c = c0_ + u_;                                          \
-        float(&x)[EPV] = xg_[u_];                                        \
-        __VA_ARGS__                                                      \
-      }                                                                  \
-    }                                                                    \
+// Unaligned rows: the 16-byte group of elements i0 .. i0+EPV-1 read element by
+// element (zeros past the end), packed as the aligned load would return it.
+template <typename T> struct GroupLoad;
+template <> struct GroupLoad<F32> {
+  __device__ static uint4 scalar(const char* rp, int i0, int V) {
+    const uint32_t* s = (const uint32_t*)rp;
+    uint32_t w[4];
+_Pragma("clang loop unroll(full)")
+    for (int k = 0; k < 4; ++k) w[k] = (i0 + k < V) ? s[i0 + k] : 0u;
+    return make_uint4(w[0], w[1], w[2], w[3]);
+  }
+};
+template <typename T> struct GroupLoad16 {
+  __device__ static uint4 scalar(const char* rp, int i0, int V) {
+    const uint16_t* s = (const uint16_t*)rp;
+    uint32_t w[4];
+_Pragma("clang loop unroll(full)")
+    for (int k = 0; k < 4; ++k) {
+      const uint32_t lo = (i0 + 2 * k < V) ? s[i0 + 2 * k] : 0u;
+      const uint32_t hi = (i0 + 2 * k + 1 < V) ? s[i0 + 2 * k + 1] : 0u;
+      w[k] = lo | (hi << 16);
+    }
+    return make_uint4(w[0], w[1], w[2], w[3]);
+  }
+};
+template <> struct GroupLoad<BF16> : GroupLoad16<BF16> {};
+template <> struct GroupLoad<F16> : GroupLoad16<F16> {};
+
+// Stream the row in steps of kRowUnroll chunks: every thread first issues its
+// kRowUnroll 16-byte loads (unconditionally; bytes past the row read as zero),
+// then decodes them (elements past the row become -inf) and runs the body on
+// `c` (chunk) and `x` (its EPV elements). Expanded in place so that the
+// accumulators stay in registers.
+constexpr int kRowUnroll = 8;
+#define ROW_FOR_GROUPS(...)                                                         \
+  for (int c0_ = 0; c0_ < nchunks; c0_ += kRowUnroll) {                            \
+    uint4 wg_[kRowUnroll];                                                          \
+    _Pragma("clang loop unroll(full)") for (int u_ = 0; u_ < kRowUnroll; ++u_)     \
+      wg_[u_] = load_raw(c0_ + u_);                                                 \
+    _Pragma("clang loop unroll(full)") for (int u_ = 0; u_ < kRowUnroll; ++u_) {   \
+      if (c0_ + u_ < nchunks) {                                                     \
+        const int c = c0_ + u_;                                                     \
+        float x[EPV];                                                               \
+        decode(wg_[u_], c, x);                                                      \
+        __VA_ARGS__                                                                 \
+      }                                                                             \
+    }                                                                               \
   }
 
 constexpr int kMaxChunks = 64;                              // chunks of 1024 x EPV elements
 constexpr int kMaxPenWords = kMaxChunks * kRowThreads * 8 / 32;  // penalty bits (V <= 524288)
 
-template <typename T>
+template <typename T, bool AL>
 __global__ __launch_bounds__(kRowThreads) void row_stats_kernel(RowParams p) {
   using RE = RowElem<T>;
   using S = typename T::storage;
@@ -267,20 +330,24 @@ __global__ __launch_bounds__(kRowThreads) void row_stats_kernel(RowParams p) {
   __shared__ uint32_t pbits[kMaxPenWords];
   const char* rp = (const char*)p.logits + (long)row * p.row_stride * (long)sizeof(S);
   const int nchunks = (p.V + kRowThreads * EPV - 1) / (kRowThreads * EPV);
+  const __amdgpu_buffer_rsrc_t rs =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(rp), (short)0, p.V * (int)sizeof(S), 0x00020000);
 
-  // Elements e of this thread's 16-byte group in chunk c (-inf past the end);
-  // rows that do not start on a 16-byte boundary are read element by element.
-  const bool aligned = (((uintptr_t)rp) & 15u) == 0;
-  auto load_group = [&](int c, float (&x)[EPV]) __attribute__((always_inline)) {
+  // The 16-byte group of chunk c of this thread (zeros past the row end).
+  auto load_raw = [&](int c) __attribute__((always_inline)) -> uint4 {
     const int i0 = (c * kRowThreads + tid) * EPV;
-    if (aligned && i0 + EPV <= p.V) {
-      const uint4 w = *(const uint4*)(rp + (long)i0 * sizeof(S));
-_Pragma("clang loop unroll(full)")
-      for (int e = 0; e < EPV; ++e) x[e] = RE::get(w, e);
+    if constexpr (AL) {
+      return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs, i0 * (int)sizeof(S), 0, 0));
     } else {
-_Pragma("clang loop unroll(full)")
-      for (int e = 0; e < EPV; ++e) x[e] = (i0 + e < p.V) ? RE::scalar(rp, i0 + e) : kNegInf;
+      return GroupLoad<T>::scalar(rp, i0, p.V);
     }
+  };
+  auto decode = [&](const uint4& w, int c, float (&x)[EPV]) __attribute__((always_inline)) {
+    const int i0 = (c * kRowThreads + tid) * EPV;
+    static_for<EPV>([&](auto ec_) __attribute__((always_inline)) {
+      constexpr int e = decltype(ec_)::value;
+      x[e] = (i0 + e < p.V) ? RE::get(w, e) : kNegInf;
+    });
   };
 
   // ---- repetition-penalty bitmask ----
@@ -314,11 +381,16 @@ _Pragma("clang loop unroll(full)")
   { const int op[2] = {0, 0}; block_reduce<2>(mx, op, sh); }
   const float m_raw = mx[0], m_pen = mx[1];
 
-  // ---- pass 2: entropy sums (base 2) and fixed-point sampling masses ----
+  // ---- pass 2: entropy sums (base 2); with sampling, the first radix level of
+  // the fixed-point masses (a histogram by the top 12 key bits) ----
   // The T = 1 sums of xp feed the top-K keys, the log-sum-exp and H_pen only.
   const bool need_pen_sums = p.topk > 0 || p.out_entropy_pen != nullptr || p.out_lse != nullptr;
+  constexpr int L0 = RE::level_bits[0];
+  if (p.do_sample) {
+    for (int t = tid; t < (1 << L0); t += kRowThreads) sh.hist0[t] = 0;
+    __syncthreads();
+  }
   float acc[4] = {0.f, 0.f, 0.f, 0.f};
-  uint64_t zq = 0;
   ROW_FOR_GROUPS(
     const int i0 = (c * kRowThreads + tid) * EPV;
     static_for<EPV>([&](auto ec_) __attribute__((always_inline)) {
@@ -335,7 +407,14 @@ _Pragma("clang loop unroll(full)")
         acc[2] += e1;
         acc[3] += e1 > 0.f ? e1 * y1 : 0.f;
       }
-      if (p.do_sample) zq += det_q((xp - m_pen) * p.samp_c);
+      if (p.do_sample) {
+        // q = floor(det_exp2(ys) * 2^40) is exactly 0 for ys < -41
+        const float ys = (xp - m_pen) * p.samp_c;
+        if (ys >= -41.0f) {
+          const uint64_t q = det_q(ys);
+          if (q) atomicAdd((unsigned long long*)&sh.hist0[RE::key(xp) >> (32 - L0)], (unsigned long long)q);
+        }
+      }
         });
     )
   { const int op[4] = {1, 1, 1, 1}; block_reduce<4>(acc, op, sh); }
@@ -392,16 +471,18 @@ _Pragma("clang loop unroll(full)")
 
   // ---- pass 4: exact temperature + top-p draw ----
   if (!p.do_sample) return;
-  const uint64_t Z = block_sum_u64(zq, sh);
-  uint64_t need = (uint64_t)(((unsigned __int128)Z * p.top_p_q32 + 0xffffffffull) >> 32);
-  if (need < 1) need = 1;
   constexpr int NLEV = RE::nlevels;
+  constexpr int LAST_BITS = RE::level_bits[NLEV - 1];
+  constexpr bool kChunkCounts = LAST_BITS <= 4;  // the final index search rides on the last level
 
   // Histogram of masses by the `bits` key bits below `done` already-fixed bits
-  // equal to `prefix`, into h (bins = 1 << bits).
-  auto histogram = [&](uint64_t* h, int done, uint32_t prefix, int bits) __attribute__((always_inline)) {
+  // equal to `prefix`, into h (bins = 1 << bits); with `counts`, also the
+  // number of such elements per (chunk, bin) into sh.cc.
+  auto histogram = [&](uint64_t* h, int done, uint32_t prefix, int bits, bool counts) __attribute__((always_inline)) {
     const int nb = 1 << bits;
     for (int t = tid; t < nb; t += kRowThreads) h[t] = 0;
+    if (counts)
+      for (int t = tid; t < kMaxChunks * 16; t += kRowThreads) sh.cc[t] = 0;
     __syncthreads();
     const int shift = 32 - done - bits;
     ROW_FOR_GROUPS(
@@ -411,33 +492,33 @@ _Pragma("clang loop unroll(full)")
         if (i0 + e >= p.V) return;
         const float xp = penal(i0 + e, x[e]);
         const uint32_t k = RE::key(xp);
-        if (done > 0 && (k >> (32 - done)) != prefix) return;
-        const uint64_t q = det_q((xp - m_pen) * p.samp_c);
-        if (q) atomicAdd((unsigned long long*)&h[(k >> shift) & (uint32_t)(nb - 1)], (unsigned long long)q);
+        if ((k >> (32 - done)) != prefix) return;
+        const uint32_t bin = (k >> shift) & (uint32_t)(nb - 1);
+        const float ys = (xp - m_pen) * p.samp_c;
+        const uint64_t q = ys >= -41.0f ? det_q(ys) : 0;
+        if (q) atomicAdd((unsigned long long*)&h[bin], (unsigned long long)q);
+        if (counts) atomicAdd(&sh.cc[c * 16 + bin], 1u);
             });
     )
     __syncthreads();
   };
-  // Bin b of h (largest bins first) with above + mass(bins > b) <= pos < above + mass(bins >= b);
-  // returns b and adds mass(bins > b) to above.
-  auto pick_bin = [&](const uint64_t* h, int bits, uint64_t pos, uint64_t& above) __attribute__((always_inline)) -> uint32_t {
+  // Scan of a histogram, bins in descending order: thread t owns bins
+  // nb-1-t*per .. nb-per-t*per; returns the mass above its bins, and the total.
+  auto scan_bins = [&](const uint64_t* h, int bits, uint64_t& total) __attribute__((always_inline)) -> uint64_t {
     const int nb = 1 << bits;
-    const int per = (nb + kRowThreads - 1) / kRowThreads;  // bins per thread, top-down
-    // thread t owns bins nb-1-t*per ... nb-1-(t*per+per-1)
+    const int per = (nb + kRowThreads - 1) / kRowThreads;
     uint64_t mine = 0;
     for (int j = 0; j < per; ++j) {
       const int b = nb - 1 - (tid * per + j);
       if (b >= 0) mine += h[b];
     }
-    sh.part[tid] = mine;
-    __syncthreads();
-    for (int off = 1; off < kRowThreads; off <<= 1) {
-      const uint64_t v = tid >= off ? sh.part[tid - off] : 0;
-      __syncthreads();
-      sh.part[tid] += v;
-      __syncthreads();
-    }
-    uint64_t run = above + sh.part[tid] - mine;  // mass of all bins above this thread's
+    return block_excl_scan_u64(mine, total, sh);
+  };
+  // The bin holding mass position pos, given each thread's `run` (mass above its
+  // bins, plus `above`); adds the mass of the bins above it to `above`.
+  auto pick_bin = [&](const uint64_t* h, int bits, uint64_t run, uint64_t pos, uint64_t& above) __attribute__((always_inline)) -> uint32_t {
+    const int nb = 1 << bits;
+    const int per = (nb + kRowThreads - 1) / kRowThreads;
     for (int j = 0; j < per; ++j) {
       const int b = nb - 1 - (tid * per + j);
       if (b < 0) break;
@@ -453,16 +534,23 @@ _Pragma("clang loop unroll(full)")
     __syncthreads();
     return b;
   };
+  // Level 0 is scanned once for both selections.
+  uint64_t Z;
+  const uint64_t run0 = scan_bins(sh.hist0, L0, Z);
+  uint64_t need = (uint64_t)(((unsigned __int128)Z * p.top_p_q32 + 0xffffffffull) >> 32);
+  if (need < 1) need = 1;
   // Key holding mass position pos (order: xp desc, index asc) and the mass above it.
-  auto select = [&](uint64_t pos, uint32_t& key_out, uint64_t& above_out) __attribute__((always_inline)) {
+  auto select = [&](uint64_t pos, bool counts, uint32_t& key_out, uint64_t& above_out) __attribute__((always_inline)) {
     uint64_t above = 0;
-    uint32_t prefix = pick_bin(sh.hist0, RE::level_bits[0], pos, above);
-    int done = RE::level_bits[0];
+    uint32_t prefix = pick_bin(sh.hist0, L0, run0, pos, above);
+    int done = L0;
     _Pragma("clang loop unroll(full)")
     for (int lev = 1; lev < NLEV; ++lev) {
       const int bits = RE::level_bits[lev];
-      histogram(sh.hist1, done, prefix, bits);
-      prefix = (prefix << bits) | pick_bin(sh.hist1, bits, pos, above);
+      histogram(sh.hist1, done, prefix, bits, counts && lev == NLEV - 1);
+      uint64_t tot;
+      const uint64_t run = scan_bins(sh.hist1, bits, tot) + above;
+      prefix = (prefix << bits) | pick_bin(sh.hist1, bits, run, pos, above);
       done += bits;
     }
     key_out = prefix << (32 - done);  // the full 32-bit key (low bits zero for bf16)
@@ -475,10 +563,9 @@ _Pragma("clang loop unroll(full)")
   // Mass of one token with key kk (every such token has the value key_to_float(kk)).
   auto key_mass = [&](uint32_t kk) -> uint64_t { return det_q((key_to_float(kk) - m_pen) * p.samp_c); };
 
-  histogram(sh.hist0, 0, 0u, RE::level_bits[0]);
   uint32_t key_n;
   uint64_t above_n;
-  select(need - 1, key_n, above_n);
+  select(need - 1, false, key_n, above_n);
   const uint64_t qn = key_mass(key_n);
   const uint64_t jn = (need - 1 - above_n) / qn;  // 0-based index of the last kept tie
   const uint64_t kept_mass = above_n + (jn + 1) * qn;
@@ -490,22 +577,28 @@ _Pragma("clang loop unroll(full)")
 
   uint32_t key_r;
   uint64_t above_r;
-  select(r, key_r, above_r);
+  select(r, kChunkCounts, key_r, above_r);
   const uint64_t qr = key_mass(key_r);
   const uint32_t j = (uint32_t)((r - above_r) / qr);  // the j-th (0-based) token of key_r by index
 
-  // The j-th token with key_r in index order: per-chunk totals, then a thread scan.
-  if (tid < kMaxChunks) sh.chunk_tot[tid] = 0;
-  __syncthreads();
-  ROW_FOR_GROUPS(
-    const int i0 = (c * kRowThreads + tid) * EPV;
-    uint32_t n = 0;
+  // The j-th token with key_r in index order: per-chunk totals, then a thread scan
+  // over the chunk that holds it.
+  if constexpr (kChunkCounts) {
+    const uint32_t lastv = (key_r >> (32 - kKeyBitsUsed)) & ((1u << LAST_BITS) - 1);
+    if (tid < kMaxChunks) sh.chunk_tot[tid] = tid < nchunks ? sh.cc[tid * 16 + lastv] : 0u;
+  } else {
+    if (tid < kMaxChunks) sh.chunk_tot[tid] = 0;
+    __syncthreads();
+    ROW_FOR_GROUPS(
+      const int i0 = (c * kRowThreads + tid) * EPV;
+      uint32_t n = 0;
 _Pragma("clang loop unroll(full)")
-    for (int e = 0; e < EPV; ++e)
-      if (i0 + e < p.V && match(penal(i0 + e, x[e]), key_r)) ++n;
-    for (int o = 32; o >= 1; o >>= 1) n += __shfl_xor(n, o);
-    if (lane == 0 && n) atomicAdd(&sh.chunk_tot[c], n);
-    )
+      for (int e = 0; e < EPV; ++e)
+        if (i0 + e < p.V && match(penal(i0 + e, x[e]), key_r)) ++n;
+      for (int o = 32; o >= 1; o >>= 1) n += __shfl_xor(n, o);
+      if (lane == 0 && n) atomicAdd(&sh.chunk_tot[c], n);
+      )
+  }
   __syncthreads();
   int cstar = 0;
   uint32_t before = 0;
@@ -514,21 +607,14 @@ _Pragma("clang loop unroll(full)")
     before += sh.chunk_tot[c];
   }
   float xs[EPV];
-  load_group(cstar, xs);
+  decode(load_raw(cstar), cstar, xs);
   const int is0 = (cstar * kRowThreads + tid) * EPV;
   uint32_t mine = 0;
 _Pragma("clang loop unroll(full)")
   for (int e = 0; e < EPV; ++e)
     if (is0 + e < p.V && match(penal(is0 + e, xs[e]), key_r)) ++mine;
-  sh.scan[tid] = (int32_t)mine;
-  __syncthreads();
-  for (int off = 1; off < kRowThreads; off <<= 1) {
-    const int32_t v = tid >= off ? sh.scan[tid - off] : 0;
-    __syncthreads();
-    sh.scan[tid] += v;
-    __syncthreads();
-  }
-  const uint32_t excl = before + (uint32_t)sh.scan[tid] - mine;
+  uint64_t tot_unused;
+  const uint32_t excl = before + (uint32_t)block_excl_scan_u64(mine, tot_unused, sh);
   if (mine && excl <= j && j < excl + mine) {
     uint32_t seen = excl;
     static_for<EPV>([&](auto ec_) __attribute__((always_inline)) {
@@ -544,9 +630,15 @@ _Pragma("clang loop unroll(full)")
 template <typename T>
 static int dispatch_rows(const RowParams& p, hipStream_t s) {
   constexpr int EPV = RowElem<T>::EPV;
+  using S = typename T::storage;
   const long nchunks = ((long)p.V + kRowThreads * EPV - 1) / (kRowThreads * EPV);
   if (nchunks > kMaxChunks || (long)p.V > (long)kMaxPenWords * 32) return MENTAT_EUNSUP;
-  hipLaunchKernelGGL((row_stats_kernel<T>), dim3(p.R), dim3(kRowThreads), 0, s, p);
+  // 16-byte loads need every row to start on a 16-byte boundary.
+  const bool aligned = (((uintptr_t)p.logits) & 15u) == 0 && ((p.row_stride * (long)sizeof(S)) & 15) == 0;
+  if (aligned)
+    hipLaunchKernelGGL((row_stats_kernel<T, true>), dim3(p.R), dim3(kRowThreads), 0, s, p);
+  else
+    hipLaunchKernelGGL((row_stats_kernel<T, false>), dim3(p.R), dim3(kRowThreads), 0, s, p);
   return (int)hipGetLastError();
 }
 
