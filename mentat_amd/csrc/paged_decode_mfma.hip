@@ -154,26 +154,47 @@ __device__ __forceinline__ float get_shared(const float* p) {
 
 // Pieces are the partial slots unit + w of waves w0..w1; lane l owns the
 // E = G*D/64 consecutive outputs starting at l*E of the unit's [G][D] block.
+// Pieces are read in batches whose loads are all in flight together, and are
+// combined in wave order, so the result does not depend on arrival order.
 template <typename T, int D, int G>
 __device__ __forceinline__ void merge_unit(const NativeParams& p, int seq, int head, long unit, int w0, int w1,
                                            int lane) {
   constexpr int E = G * D / 64;
   static_assert(E >= 1, "merge lane split");
+  constexpr int KB = E >= 32 ? 1 : (E >= 16 ? 2 : 4);  // pieces per batch
   const int g = (lane * E) / D;
   const int d0 = (lane * E) - g * D;
-  float M = kNegInf;
-  for (int w = w0; w <= w1; ++w) M = fmaxf(M, get_shared(p.ws_ml + ((unit + w) * G + g) * 2));
-  const float ms = (M == kNegInf) ? 0.f : M;
-  float L = 0.f, acc[E];
+  const int n = w1 - w0 + 1;
+  float M = kNegInf, L = 0.f, acc[E];
 #pragma unroll
   for (int e = 0; e < E; ++e) acc[e] = 0.f;
-  for (int w = w0; w <= w1; ++w) {
-    const long slot = unit + w;
-    const float c = fast_exp2(get_shared(p.ws_ml + (slot * G + g) * 2) - ms);
-    L += get_shared(p.ws_ml + (slot * G + g) * 2 + 1) * c;
-    const float* wo = p.ws_o + (slot * G + g) * D + d0;
+  for (int k0 = 0; k0 < n; k0 += KB) {
+    float mk[KB], lk[KB], ok[KB][E];
+    // Past-the-end entries of the last batch reload piece n-1 and are dropped.
+    static_for<KB>([&](auto i) {
+      const long slot = unit + w0 + min(k0 + (int)i, n - 1);
+      mk[i] = get_shared(p.ws_ml + (slot * G + g) * 2);
+      lk[i] = get_shared(p.ws_ml + (slot * G + g) * 2 + 1);
+      const float* wo = p.ws_o + (slot * G + g) * D + d0;
 #pragma unroll
-    for (int e = 0; e < E; ++e) acc[e] += get_shared(wo + e) * c;
+      for (int e = 0; e < E; ++e) ok[i][e] = get_shared(wo + e);
+    });
+    float Mn = M;
+    static_for<KB>([&](auto i) {
+      if (k0 + (int)i < n) Mn = fmaxf(Mn, mk[i]);
+    });
+    const float ms = (Mn == kNegInf) ? 0.f : Mn;
+    const float cold = (M == kNegInf) ? 0.f : fast_exp2(M - ms);
+    L *= cold;
+#pragma unroll
+    for (int e = 0; e < E; ++e) acc[e] *= cold;
+    static_for<KB>([&](auto i) {
+      const float c = (k0 + (int)i < n && mk[i] != kNegInf) ? fast_exp2(mk[i] - ms) : 0.f;
+      L += lk[i] * c;
+#pragma unroll
+      for (int e = 0; e < E; ++e) acc[e] += ok[i][e] * c;
+    });
+    M = Mn;
   }
   const float inv = L > 0.f ? 1.f / L : 0.f;
   const long ob = ((long)seq * p.Hq + (long)head * G + g) * D + d0;
@@ -400,8 +421,53 @@ __global__ __launch_bounds__(kNativeThreads) void paged_decode_mfma_kernel(Nativ
   }
 }
 
+// Persistent grid size of one kernel instantiation: its resident wavefronts on
+// the current device (CUs x resident workgroups x 4), cached per device.
 template <typename T, int D, int G, int B>
-static int launch_native(const NativeParams& p, hipStream_t stream) {
+static int persistent_waves() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+  if (cached[dev] > 0) return cached[dev];
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+    cus = 256;
+  int blocks = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, paged_decode_mfma_kernel<T, D, G, B>,
+                                                   kNativeThreads, 0) != hipSuccess || blocks <= 0)
+    blocks = 1;
+  cached[dev] = cus * blocks * (kNativeThreads / 64);
+  return cached[dev];
+}
+
+// The largest persistent grid over the instantiations a call with this head
+// geometry may use; the workspace holds one partial slot per wavefront.
+template <int D, int G>
+static int max_persistent_waves() {
+  return max(max(max(persistent_waves<BF16, D, G, 16>(), persistent_waves<BF16, D, G, 32>()),
+                 persistent_waves<BF16, D, G, 64>()),
+             max(max(persistent_waves<F16, D, G, 16>(), persistent_waves<F16, D, G, 32>()),
+                 persistent_waves<F16, D, G, 64>()));
+}
+static int workspace_waves(int D, int G) {
+  switch (D * 100 + G) {
+    case 6401: return max_persistent_waves<64, 1>();
+    case 6402: return max_persistent_waves<64, 2>();
+    case 6404: return max_persistent_waves<64, 4>();
+    case 6408: return max_persistent_waves<64, 8>();
+    case 6416: return max_persistent_waves<64, 16>();
+    case 12801: return max_persistent_waves<128, 1>();
+    case 12802: return max_persistent_waves<128, 2>();
+    case 12804: return max_persistent_waves<128, 4>();
+    case 12808: return max_persistent_waves<128, 8>();
+    case 12816: return max_persistent_waves<128, 16>();
+    default: return 0;
+  }
+}
+
+template <typename T, int D, int G, int B>
+static int launch_native(NativeParams p, hipStream_t stream) {
+  p.W = persistent_waves<T, D, G, B>();  // <= the workspace's wave count
   hipLaunchKernelGGL((paged_decode_mfma_kernel<T, D, G, B>), dim3(p.W / 4), dim3(kNativeThreads), 0, stream, p);
   return (int)hipGetLastError();
 }
@@ -437,24 +503,6 @@ static int native_d(int D, int G, const NativeParams& p, hipStream_t s) {
   }
 }
 
-// Persistent grid size: resident wavefronts of the current device, rounded to
-// whole workgroups. Cached per device.
-static int persistent_waves() {
-  static int cached[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
-  if (cached[dev] > 0) return cached[dev];
-  int cus = 0;
-  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
-    cus = 256;
-  int blocks = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, paged_decode_mfma_kernel<BF16, 128, 4, 16>,
-                                                   kNativeThreads, 0) != hipSuccess || blocks <= 0)
-    blocks = 2;
-  cached[dev] = cus * blocks * (kNativeThreads / 64);
-  return cached[dev];
-}
-
 }  // namespace mentat
 
 using namespace mentat;
@@ -462,8 +510,8 @@ using namespace mentat;
 // Workspace of the native path: the reserved counters, then the partial
 // slots (units + waves).
 size_t native_workspace_bytes(int N, int Hq, int Hkv, int D) {
-  const int W = persistent_waves();
   const int G = Hq / Hkv;
+  const int W = workspace_waves(D, G);
   const size_t slots = (size_t)N * Hkv + W;
   return kWsReserved + slots * G * (D + 2) * sizeof(float);
 }
@@ -481,9 +529,10 @@ int native_paged_decode(const void* q, const void* k_cache, const void* v_cache,
   p.q = q; p.k = k_cache; p.v = v_cache;
   p.tables = block_tables; p.table_stride = table_stride; p.rows = seq_rows; p.lens = seq_lens;
   p.num_blocks = num_blocks; p.out = out;
-  p.N = N; p.Hq = Hq; p.Hkv = Hkv; p.B = block_size; p.W = persistent_waves();
-  p.scale_log2 = scale * kLog2e;
   const int G = Hq / Hkv;
+  p.N = N; p.Hq = Hq; p.Hkv = Hkv; p.B = block_size; p.W = workspace_waves(D, G);
+  if (p.W <= 0) return MENTAT_EUNSUP;
+  p.scale_log2 = scale * kLog2e;
   const size_t slots = (size_t)N * Hkv + p.W;
   p.ctr = (int32_t*)workspace;
   p.ws_o = (float*)((char*)workspace + kWsReserved);

@@ -265,7 +265,6 @@ __device__ __forceinline__ void tree_shared(const TreeParams& p, const int32_t* 
   const int row = tld(item, 0), t_first = tld(item, 1), ntile = tld(item, 2), valid = tld(item, 3);
   const int head = tld(item, 4), nmem = tld(item, 5), slot0 = tld(item, 6), moff = tld(item, 7);
   if (ntile <= 0 || ntile > kTreeSharedMaxTiles || nmem <= 0) return;  // uniform over the workgroup
-  const int t_last = t_first + ntile;
   const int32_t* trow = p.tables + (long)row * p.table_stride;
 
   // Block ids of the task's tiles, read once into scalar registers (tiles
