@@ -80,6 +80,10 @@ class MentatBatchGenerator(MentatGenerator):
                 live.append(run)
 
         admit()
+        if self.wrapper.graphs is not None:
+            lens = [len(self.tokenizer(p, return_tensors="pt")["input_ids"][0]) if isinstance(p, str) else len(p)
+                    for p in prompts]
+            self._prepare_capture(max_trees, max(lens))
         t_start = time.perf_counter()
         prefill_before = prefill_s
         while live:

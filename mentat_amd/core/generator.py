@@ -62,6 +62,7 @@ class MentatGenerator:
         soft_explore_initial: float = 0.3,
         gate: str = "relative",
         entropy_threshold: float = 2.0,
+        capture_steps: bool = True,
     ):
         if gate not in ("relative", "absolute"):
             raise ValueError("gate must be 'relative' or 'absolute'")
@@ -102,6 +103,8 @@ class MentatGenerator:
             dtype=adapter.dtype,
         )
         self.wrapper = PagedModelWrapper(model, self.kv_cache_mgr, adapter, eos_token_id=eos)
+        if capture_steps and self.wrapper.device.type == "cuda":
+            self.wrapper.enable_step_capture()
 
         self.branch_points: list[tuple[int, float, int]] = []
         self.pruning_events: list[tuple[int, int]] = []
@@ -144,6 +147,7 @@ class MentatGenerator:
                          cumulative_log_prob=0.0, depth=0, is_active=True)
         tree.root.children[0] = first
         self._decide(tree, [first], logits.unsqueeze(0), step=0, num_active=1)
+        self._prepare_capture(1, int(input_ids.shape[-1]))
 
         t0 = time.perf_counter()
         for step in range(1, self.max_new_tokens):
@@ -182,6 +186,21 @@ class MentatGenerator:
         results.sort(key=lambda r: r["norm_prob"], reverse=True)
         self.tree = tree
         return results
+
+    def max_leaves_per_tree(self) -> int:
+        """Live leaves one tree can reach: every leaf of a step decides against the
+        step's frozen num_active, so with a live leaves (a <= M - K) all of them
+        may branch into K children each."""
+        return max(self.M, (self.M - self.K) * self.K, 1)
+
+    def _prepare_capture(self, trees: int, max_prompt: int) -> None:
+        """Capture the decode steps' batch buckets before the decode timer starts."""
+        graphs = self.wrapper.graphs
+        if graphs is None:
+            return
+        leaves = trees * self.max_leaves_per_tree()
+        graphs.prepare(leaves, max_prompt + self.max_new_tokens + 1, rows=leaves + trees)
+        torch.cuda.synchronize(self.wrapper.device)
 
     # ------------------------------------------------------------------
     def _penalty_csr(self, leaves: list[TreeNode]):

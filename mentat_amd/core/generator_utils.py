@@ -191,6 +191,15 @@ class PagedModelWrapper:
         self.device = adapter.device
         self.dtype = adapter.dtype
         self.config = model.config
+        self.graphs = None
+
+    def enable_step_capture(self) -> None:
+        """Run batched decode steps as captured graph replays (core/graph_decode.py);
+        batches above its largest bucket still run eagerly."""
+        from .graph_decode import DecodeGraphs
+
+        if self.graphs is None:
+            self.graphs = DecodeGraphs(self)
 
     @torch.no_grad()
     def prefill(self, input_ids: torch.LongTensor, seq_id: int) -> torch.Tensor:
@@ -219,6 +228,10 @@ class PagedModelWrapper:
         if N == 0:
             return (torch.empty(0, self.config.vocab_size, device=self.device, dtype=self.dtype),
                     torch.empty(0, self.config.hidden_size, device=self.device, dtype=self.dtype))
+        if self.graphs is not None:
+            out = self.graphs.decode(token_ids_per_seq, seq_ids)
+            if out is not None:
+                return out
         ids = torch.tensor(token_ids_per_seq, dtype=torch.long).to(self.device).unsqueeze(0)
         hidden = a.embeddings(ids)
         offsets = [self.kv_cache_mgr.get_kv_length(s) for s in seq_ids]  # RoPE position of the new token

@@ -1,0 +1,193 @@
+"""Captured decode steps: one HIP graph launch per batched decode forward.
+
+The eager decode step (PagedModelWrapper.decode_batch_tensor, the reference's
+core/generator_utils.py:340-418 loop) launches ~30 kernels per layer from
+Python, and at Llama-3-8B size with ~150 live leaves the host, not the GPU,
+sets the step time. Here the whole forward for a batch of ``Nb`` sequences —
+embedding, every layer's norm, Q/K/V projections, RoPE, KV append (with the
+lazy copy-on-write), paged decode attention, output projection, MLP and
+residuals, the final norm and the LM head — is captured once per batch-size
+bucket ``Nb`` and replayed per step.
+
+Per step the host does what must stay on the host: the allocator and page
+tables of every layer in one call (PagedKVCacheManager.plan_append_step, the
+same block ids as the per-layer loop), then one pinned host-to-device copy of
+the step's int32 inputs (token ids, RoPE positions, table rows and the
+[num_layers, 7, Nb] append plans) and one graph replay. Batches are padded to
+the bucket: padding entries carry the token 0 at position 0, read the
+manager's length-0 row (their attention output is zero) and have append plans
+whose destination block is -1, which the append kernel skips; their logits are
+dropped.
+
+A captured graph holds the addresses of the manager's device tables, of the
+K/V stores, of its own input buffer and of the paged-decode workspace, so
+  * graphs are captured again after the manager reallocates its tables
+    (``tables_version``); ``prepare`` reserves table capacity up front;
+  * the decode workspace of the capture stream is sized for the largest
+    bucket before the first capture, and this object keeps it alive.
+Warm-up and capture run with an all-padding input, which writes nothing to
+the cache.
+"""
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from .. import ops
+from .._lib import get_lib
+
+__all__ = ["DecodeGraphs", "BUCKETS"]
+
+# Batch-size buckets (a step of N sequences runs the smallest bucket >= N).
+BUCKETS = (8, 16, 32, 48, 64, 96, 128, 160, 192, 256)
+
+
+class _Bucket:
+    __slots__ = ("n", "graph", "dev", "host", "host_np", "logits", "hidden", "version")
+
+
+class DecodeGraphs:
+    """Captured batched decode forwards for one PagedModelWrapper."""
+
+    def __init__(self, wrapper, buckets=BUCKETS):
+        self.w = wrapper
+        self.a = wrapper.adapter
+        self.m = wrapper.kv_cache_mgr
+        self.dev = wrapper.device
+        self.buckets = tuple(sorted(buckets))
+        self.max_batch = self.buckets[-1]
+        self._graphs: dict[int, _Bucket] = {}
+        self._stream = torch.cuda.Stream(self.dev)
+        self._ws = None
+        self.captures = 0
+
+    # ------------------------------------------------------------------
+    def bucket(self, n: int):
+        for b in self.buckets:
+            if b >= n:
+                return b
+        return None
+
+    def prepare(self, max_batch: int, max_len: int, rows: int = 0) -> None:
+        """Reserve table capacity for sequences of up to ``max_len`` tokens and
+        ``rows`` more live sequences, and capture every bucket up to the one
+        that holds ``max_batch``."""
+        m = self.m
+        m.reserve(rows, -(-max_len // m.block_size))
+        top = self.bucket(min(max_batch, self.max_batch))
+        for b in self.buckets:
+            if b <= top:
+                self._get(b)
+
+    # ------------------------------------------------------------------
+    def _inputs_layout(self, nb: int):
+        L = self.m.num_layers
+        return 3 * nb + L * 7 * nb
+
+    def _fill_padding(self, h: np.ndarray, nb: int, n: int) -> None:
+        """Entries n..nb-1 of every field become padding."""
+        L = self.m.num_layers
+        h[n:nb] = 0                        # token ids
+        h[nb + n: 2 * nb] = 0              # positions
+        h[2 * nb + n: 3 * nb] = self.m.empty_row()
+        plans = h[3 * nb:].reshape(L, 7, nb)
+        plans[:, :, n:] = -1               # dst block -1: skipped by the append kernel
+        plans[:, 6, n:] = 0
+
+    def _forward(self, buf: torch.Tensor, nb: int):
+        a, m = self.a, self.m
+        L = m.num_layers
+        ids = buf[0:nb].long().unsqueeze(0)            # [1, nb]
+        pos = buf[nb:2 * nb].long().unsqueeze(1)       # [nb, 1]
+        rows = buf[2 * nb:3 * nb]                      # [nb] int32
+        plans = buf[3 * nb:].view(L, 7, nb)
+        max_seqlen = m._pages_cap * m.block_size
+        hidden = a.embeddings(ids)
+        for layer_idx, block in enumerate(a.layers):
+            attn = a.get_self_attn(block)
+            residual = hidden
+            x = a.apply_pre_attn_norm(block, hidden)
+            hs = x.squeeze(0).unsqueeze(1)             # [nb, 1, hidden]: one token per sequence
+            q, k, v = a.project_qkv(attn, hs)
+            q, k = a.apply_rope(attn, q, k, pos, v_for_shape=v)
+            ops.kv_append(k.squeeze(1).to(m.dtype).contiguous(), v.squeeze(1).to(m.dtype).contiguous(),
+                          m._k_store, m._v_store, plans[layer_idx], block_size=m.block_size, layout=m.layout,
+                          block_tables=m._tables[layer_idx], seq_lens=m._lens[layer_idx])
+            o = ops.paged_decode(q.squeeze(1).contiguous(), m._k_store, m._v_store, layout=m.layout,
+                                 block_tables=m._tables[layer_idx], seq_lens=m._lens[layer_idx], seq_rows=rows,
+                                 max_seqlen=max_seqlen)
+            attn_out = attn.o_proj(o.reshape(1, nb, -1))
+            hidden = a.apply_post_attn_residual(block, residual, attn_out)
+            residual = hidden
+            x = a.apply_pre_mlp_norm(block, hidden)
+            hidden = a.apply_post_mlp_residual(block, residual, a.get_mlp(block)(x))
+        hidden = a.final_norm(hidden).squeeze(0)
+        return a.lm_head(hidden), hidden
+
+    def _workspace(self) -> None:
+        """Size the capture stream's decode workspace for the largest bucket."""
+        if self._ws is not None:
+            return
+        a, m = self.a, self.m
+        nbytes = get_lib().mentat_paged_decode_workspace_bytes(
+            m.layout, self.max_batch, a.num_attention_heads, a.num_key_value_heads, a.head_dim, m.block_size,
+            m._pages_cap * m.block_size, 0)
+        with torch.cuda.stream(self._stream):
+            self._ws = ops.workspace(self.dev, nbytes)
+
+    def _get(self, nb: int) -> _Bucket:
+        b = self._graphs.get(nb)
+        if b is not None and b.version == self.m.tables_version:
+            return b
+        self._graphs.pop(nb, None)
+        self._workspace()
+        m = self.m
+        size = self._inputs_layout(nb)
+        b = _Bucket()
+        b.n = nb
+        b.host = torch.empty(size, dtype=torch.int32, pin_memory=True)
+        b.host_np = b.host.numpy()
+        self._fill_padding(b.host_np, nb, 0)
+        b.dev = torch.empty(size, dtype=torch.int32, device=self.dev)
+        b.dev.copy_(b.host)
+        s = self._stream
+        s.wait_stream(torch.cuda.current_stream(self.dev))
+        with torch.cuda.stream(s):
+            for _ in range(2):  # warm-up (library handles, GEMM selection) on all-padding input
+                self._forward(b.dev, nb)
+        torch.cuda.current_stream(self.dev).wait_stream(s)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            b.logits, b.hidden = self._forward(b.dev, nb)
+        torch.cuda.current_stream(self.dev).wait_stream(s)
+        b.graph = g
+        b.version = m.tables_version
+        self._graphs[nb] = b
+        self.captures += 1
+        return b
+
+    # ------------------------------------------------------------------
+    def decode(self, token_ids: list[int], seq_ids: list[int]):
+        """The step of PagedModelWrapper.decode_batch_tensor: (logits [N, V],
+        final hidden [N, hidden]); returns None when N exceeds the largest
+        bucket (the caller runs the eager step)."""
+        n = len(seq_ids)
+        nb = self.bucket(n)
+        if nb is None:
+            return None
+        m = self.m
+        offsets = [m.get_kv_length(s) for s in seq_ids]  # RoPE positions: lengths before the append
+        rows = [m._sequences[s].row for s in seq_ids]
+        plan = m.plan_append_step(seq_ids)                # [L, 7, n]
+        m._ensure_pages(int(plan[:, 4].max()) + 1)
+        b = self._get(nb)
+        h = b.host_np
+        L = m.num_layers
+        h[0:n] = token_ids
+        h[nb:nb + n] = offsets
+        h[2 * nb:2 * nb + n] = rows
+        h[3 * nb:].reshape(L, 7, nb)[:, :, :n] = plan
+        self._fill_padding(h, nb, n)
+        b.dev.copy_(b.host, non_blocking=True)
+        b.graph.replay()
+        return b.logits[:n].clone(), b.hidden[:n].clone()

@@ -198,6 +198,10 @@ class PagedKVCacheManager:
         self._free_rows: list[int] = list(range(self._rows_cap - 1, -1, -1))
         self._rows_cache: dict[tuple, torch.Tensor] = {}
         self._cu_cache: dict[tuple, torch.Tensor] = {}
+        # Bumped whenever _tables / _lens are reallocated: captured launches that
+        # hold their addresses must be captured again.
+        self.tables_version = 0
+        self._empty_row = -1
 
         self._sequences: dict[int, SequenceState] = {}
         self._next_seq_id = 0
@@ -214,6 +218,7 @@ class PagedKVCacheManager:
         n[:, :old] = self._lens
         self._tables, self._lens, self._rows_cap = t, n, new
         self._free_rows = list(range(new - 1, old - 1, -1)) + self._free_rows
+        self.tables_version += 1
 
     def _ensure_pages(self, npages: int) -> None:
         if npages <= self._pages_cap:
@@ -225,6 +230,22 @@ class PagedKVCacheManager:
         t[:, :, : self._pages_cap] = self._tables
         self._tables, self._pages_cap = t, new
         self._rows_cache.clear()
+        self.tables_version += 1
+
+    def reserve(self, rows: int, pages: int) -> None:
+        """Grow the device tables to at least ``rows`` free rows and ``pages``
+        pages per row now, so that later steps do not reallocate them."""
+        while len(self._free_rows) < rows:
+            self._grow_rows()
+        self._ensure_pages(pages)
+
+    def empty_row(self) -> int:
+        """A table row that no sequence owns and whose length is 0 in every
+        layer (decode of a padding entry reads nothing and writes zeros)."""
+        if self._empty_row < 0:
+            self._empty_row = self._take_row()
+            self._lens[:, self._empty_row] = 0
+        return self._empty_row
 
     def _take_row(self) -> int:
         if not self._free_rows:
@@ -347,6 +368,82 @@ class PagedKVCacheManager:
             lens.append(nt[L])
         return np.array([dst, slots, cows, rows, pages, lens, list(range(len(seq_ids)))],
                         dtype=np.int32).reshape(7, len(seq_ids))
+
+    def plan_append_step(self, seq_ids: list[int]) -> np.ndarray:
+        """Host half of one decode step's appends for every layer: the int32
+        [num_layers, 7, N] plans that ``plan_append_batched(seq_ids, l)`` for
+        l = 0, 1, ... would return, with the same allocator calls in the same
+        order (layer-major, sequence-minor), so block ids and refcounts match.
+
+        Decode, prefill, fork and free act on every layer alike, so every layer
+        of a sequence has the same counters, the same refcount on its tail and
+        the same tail-sharing partition across the batch. Then layer l makes
+        the allocations layer 0 makes, at the same sequences: layer 0 is planned
+        exactly, and the other layers replay its new-page and copy-on-write
+        events on their own tables. The precondition is checked per step
+        (counters, tail refcounts, sharing partition); if it does not hold the
+        layers are planned one by one.
+        """
+        L = self.num_layers
+        N = len(seq_ids)
+        if N == 0:
+            return np.zeros((L, 7, 0), dtype=np.int32)
+        seqs = [self._sequences[s] for s in seq_ids]
+        rc = self.allocator.refcounts
+        uniform = all(s.num_tokens.count(s.num_tokens[0]) == L
+                      and s.tokens_in_last_block.count(s.tokens_in_last_block[0]) == L for s in seqs)
+        tails = []
+        if uniform:
+            tails0 = [s.page_table[0][-1] if s.page_table[0] else -1 for s in seqs]
+            rc0 = [rc[t] if t >= 0 else 0 for t in tails0]
+            shared0 = any(r > 1 for r in rc0)
+            ngroups0 = len(set(tails0))
+            tails.append(tails0)
+            for l in range(1, L):
+                tl = [s.page_table[l][-1] if s.page_table[l] else -1 for s in seqs]
+                if [rc[t] if t >= 0 else 0 for t in tl] != rc0:
+                    uniform = False
+                    break
+                if shared0 and not (len(set(tl)) == ngroups0 == len(set(zip(tails0, tl)))):
+                    uniform = False
+                    break
+                tails.append(tl)
+        if not uniform:
+            return np.stack([self.plan_append_batched(seq_ids, l) for l in range(L)])
+
+        plan = np.empty((L, 7, N), dtype=np.int32)
+        pages_before = [len(s.page_table[0]) for s in seqs]
+        p0 = self.plan_append_batched(seq_ids, 0)
+        plan[0] = p0
+        # Layer 0's events, in batch order: a new tail page, and/or a copy-on-write.
+        new_at = [i for i, s in enumerate(seqs) if len(s.page_table[0]) > pages_before[i]]
+        cow_at = [i for i in range(N) if p0[2, i] >= 0]
+        events = sorted([(i, 0) for i in new_at] + [(i, 1) for i in cow_at])
+        alloc, release = self.allocator.alloc, self.allocator.release
+        for l in range(1, L):
+            cows = [-1] * N
+            dst = tails[l]  # the tail pages, replaced below where an event gives a new one
+            for i, kind in events:
+                table = seqs[i].page_table[l]
+                if kind == 0:
+                    dst[i] = alloc()
+                    table.append(dst[i])
+                else:
+                    old = table[-1]
+                    dst[i] = alloc()
+                    release(old)
+                    table[-1] = dst[i]
+                    cows[i] = old
+            pl = plan[l]
+            pl[0] = dst
+            pl[1] = p0[1]
+            pl[2] = cows
+            pl[3:] = p0[3:]
+        # Layer 0's counters are the step's counters for every layer.
+        for s in seqs:
+            s.tokens_in_last_block[1:] = [s.tokens_in_last_block[0]] * (L - 1)
+            s.num_tokens[1:] = [s.num_tokens[0]] * (L - 1)
+        return plan
 
     def _launch_append(self, layer_idx: int, k: torch.Tensor, v: torch.Tensor, plan: np.ndarray) -> None:
         if plan.shape[1] == 0:

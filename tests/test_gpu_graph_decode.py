@@ -1,0 +1,142 @@
+"""Captured decode steps (core/graph_decode.py) against the eager step.
+
+Two managers receive the same prompts, forks, frees and decode steps; one
+wrapper runs the eager forward, the other replays captured graphs (batches
+padded to buckets, all layers' append plans from plan_append_step). Every
+step checks, on the GPU:
+  * logits and final hidden of the N real rows against the eager step
+    (bf16 model: rows padded into a larger GEMM may take another GEMM
+    kernel, so values agree to bf16 rounding, not bit for bit);
+  * the device block tables and lengths of every layer: bit-exact (the host
+    plans are the same integers);
+  * the length-0 padding row stays 0 in every layer.
+Replays alternate with eager work (forks, frees, other buckets) and every
+replay is checked. A rollout test then compares whole generator runs with
+and without capture.
+"""
+import os
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+sys.path.insert(0, GOLDEN)
+
+
+def _bf16_model():
+    from transformers import LlamaConfig, LlamaForCausalLM
+
+    cfg = LlamaConfig(hidden_size=512, num_hidden_layers=2, num_attention_heads=8, num_key_value_heads=2,
+                      head_dim=128, intermediate_size=1024, vocab_size=4096, max_position_embeddings=4096,
+                      initializer_range=0.05, tie_word_embeddings=False)
+    cfg.rope_parameters = {"rope_theta": 10000.0, "rope_type": "default"}
+    torch.manual_seed(3)
+    return LlamaForCausalLM(cfg).to(torch.bfloat16).to("cuda").eval()
+
+
+def _wrapper(model, capture):
+    from mentat_amd.adapters.adapter_factory import get_adapter
+    from mentat_amd.core.generator_utils import PagedModelWrapper
+    from mentat_amd.core.paged_kv_cache import PagedKVCacheManager
+
+    a = get_adapter(model)
+    m = PagedKVCacheManager(a.num_hidden_layers, a.num_key_value_heads, a.head_dim, max_blocks=2048, block_size=16,
+                            device="cuda", dtype=torch.bfloat16)
+    w = PagedModelWrapper(model, m, a)
+    if capture:
+        w.enable_step_capture()
+    return w
+
+
+def test_captured_steps_match_eager_steps(gpu):
+    print("case graph decode vs eager, bf16 2-layer llama", flush=True)
+    model = _bf16_model()
+    we, wg = _wrapper(model, False), _wrapper(model, True)
+    rng = np.random.default_rng(0)
+    live = []
+    with torch.no_grad():
+        for p in range(3):
+            ids = torch.tensor([rng.integers(0, 4096, 20 + 13 * p).tolist()], device="cuda")
+            se, sg = we.kv_cache_mgr.allocate_sequence(), wg.kv_cache_mgr.allocate_sequence()
+            assert se == sg
+            we.prefill(ids, se)
+            wg.prefill(ids, sg)
+            live.append(se)
+        last = {s: 1 for s in live}
+        sizes = []
+        for step in range(24):
+            # forks (shared tails: copy-on-write inside the captured append) and frees
+            if step % 5 == 1:
+                for parent in list(live)[: 2 + step // 5]:
+                    for _ in range(3):
+                        c = we.kv_cache_mgr.fork_sequence(parent)
+                        assert wg.kv_cache_mgr.fork_sequence(parent) == c
+                        live.append(c)
+                        last[c] = last[parent]
+                    live.remove(parent)
+                    we.kv_cache_mgr.free_sequence(parent)
+                    wg.kv_cache_mgr.free_sequence(parent)
+            if step % 7 == 6 and len(live) > 4:
+                s = live.pop(3)
+                we.kv_cache_mgr.free_sequence(s)
+                wg.kv_cache_mgr.free_sequence(s)
+            toks = [last[s] for s in live]
+            le, he = we.decode_batch_tensor(toks, live)
+            lg, hg = wg.decode_batch_tensor(toks, live)
+            sizes.append(len(live))
+            assert lg.shape == le.shape and hg.shape == he.shape
+            scale = float(le.float().abs().max())
+            err = float((lg.float() - le.float()).abs().max())
+            assert err <= 2e-2 * scale + 2e-2, (step, len(live), err, scale)
+            assert float((hg.float() - he.float()).abs().max()) <= 5e-2 * float(he.float().abs().max()) + 2e-2
+            me, mg = we.kv_cache_mgr, wg.kv_cache_mgr
+            rows_e = [me._sequences[s].row for s in live]
+            rows_g = [mg._sequences[s].row for s in live]
+            for layer in range(me.num_layers):
+                npg = max(len(me._sequences[s].page_table[layer]) for s in live)
+                te = me._tables[layer][rows_e, :npg].cpu()
+                tg = mg._tables[layer][rows_g, :npg].cpu()
+                assert torch.equal(te, tg), (step, layer)
+                assert torch.equal(me._lens[layer][rows_e].cpu(), mg._lens[layer][rows_g].cpu())
+            assert int(mg._lens[:, mg.empty_row()].abs().sum()) == 0
+            for s in live:
+                assert me._sequences[s].page_table == mg._sequences[s].page_table
+            last = {s: int(t) for s, t in zip(live, le.float().argmax(-1).tolist())}
+    g = wg.graphs
+    used = {g.bucket(n) for n in sizes}
+    assert len(used) >= 3, sizes                     # several buckets were replayed in turn
+    assert g.captures == len(used), (g.captures, used)  # each captured once, then replayed
+
+
+@pytest.mark.parametrize("gate,thr", [("absolute", 2.0)])
+def test_rollouts_with_and_without_capture(gpu, gate, thr):
+    import make_cfg1_trajectory as mk
+    from mentat_amd.core.batch_generator import MentatBatchGenerator
+
+    print(f"case rollout capture on/off gate={gate}", flush=True)
+    model = mk.build_model().to("cuda")
+    prompts = [np.random.default_rng(s).integers(0, 32000, 40 + 7 * s).tolist() for s in range(3)]
+    knobs = dict(max_active_branches=6, branching_factor=3, max_new_tokens=24, block_size=16, max_blocks=4096,
+                 gate=gate, entropy_threshold=thr)
+    out = {}
+    with torch.no_grad():
+        for cap in (False, True):
+            bg = MentatBatchGenerator(model, mk.StubTokenizer(prompts[0]), capture_steps=cap, **knobs)
+            res = bg.generate_batch(prompts, max_trees=2)
+            out[cap] = (res, bg.get_batch_diagnostics(), bg)
+            assert bg.kv_cache_mgr.allocator.num_used == 0
+    (r0, d0, _), (r1, d1, b1) = out[False], out[True]
+    assert b1.wrapper.graphs is not None and b1.wrapper.graphs.captures > 0
+    assert out[False][2].wrapper.graphs is None
+    for a, b in zip(r0, r1):
+        assert [x["token_ids"] for x in a] == [x["token_ids"] for x in b]
+        for x, y in zip(a, b):
+            assert abs(x["log_prob"] - y["log_prob"]) < 1e-4
+    assert d0["decode_tokens_total"] == d1["decode_tokens_total"]
+    for p in d0["prompts"]:
+        assert d0["prompts"][p]["active_branch_trace"] == d1["prompts"][p]["active_branch_trace"]
+        assert [x[::2] for x in d0["prompts"][p]["branch_points"]] == \
+            [x[::2] for x in d1["prompts"][p]["branch_points"]]

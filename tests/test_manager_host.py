@@ -166,3 +166,74 @@ def test_find_blocked_tokens_closed_forms():
                 if len(ids) >= n and ids[i:i + n - 1] == ids[len(ids) - n + 1:]:
                     want.add(ids[i + n - 1])
         assert _find_blocked_tokens(ids, mx) == want
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_plan_append_step_equals_layer_by_layer_plans(seed):
+    """One decode step planned for all layers at once (plan_append_step) gives
+    the plans, block ids, refcounts, free set and counters of plan_append_batched
+    called layer by layer, on random traces with forks (shared tails, so
+    copy-on-write), frees and page boundaries; the oracle checks the same."""
+    rng = random.Random(100 + seed)
+    L, nb, B = 5, 4096, 4
+    step = PagedKVCacheManager(L, 2, 16, max_blocks=nb, block_size=B, device="cpu", dtype=torch.float32)
+    ref = PagedKVCacheManager(L, 2, 16, max_blocks=nb, block_size=B, device="cpu", dtype=torch.float32)
+    c = OracleCache(L, nb, B)
+    n_steps = 0
+    for _ in range(200):
+        live = list(c.tables)
+        op = rng.random()
+        if not live or op < 0.12:
+            n = rng.randint(0, 9)
+            sa, sb, sc = step.allocate_sequence(), ref.allocate_sequence(), c.allocate()
+            for l in range(L):
+                step.plan_append(sa, l, n)
+                ref.plan_append(sb, l, n)
+                c.append(sc, l, list(range(n)))
+        elif op < 0.35:
+            p = rng.choice(live)
+            for _k in range(rng.randint(1, 3)):
+                assert step.fork_sequence(p) == ref.fork_sequence(p) == c.fork(p)
+            if rng.random() < 0.5 and len(live) > 1:  # the branch parent is freed after its forks
+                step.free_sequence(p)
+                ref.free_sequence(p)
+                c.free(p)
+        elif op < 0.45 and len(live) > 1:
+            s = rng.choice(live)
+            step.free_sequence(s)
+            ref.free_sequence(s)
+            c.free(s)
+        else:
+            batch = rng.sample(live, rng.randint(1, len(live)))
+            got = step.plan_append_step(batch)
+            want = np.stack([ref.plan_append_batched(batch, l) for l in range(L)])
+            for l in range(L):
+                c.append_batched(batch, l, list(range(len(batch))))
+            assert got.dtype == np.int32 and got.shape == (L, 7, len(batch))
+            assert (got == want).all()
+            n_steps += 1
+        assert step.allocator.refcounts == ref.allocator.refcounts
+        assert step.allocator._free == ref.allocator._free
+        for sid, st in step._sequences.items():
+            rt = ref._sequences[sid]
+            assert (st.page_table, st.num_tokens, st.tokens_in_last_block) == \
+                (rt.page_table, rt.num_tokens, rt.tokens_in_last_block)
+        _same_state(step, c)
+    assert n_steps > 40
+
+
+def test_plan_append_step_non_uniform_layers_fall_back():
+    """Layers appended unevenly (not what decode, prefill or fork do) take the
+    layer-by-layer path and still match it exactly."""
+    L, B = 3, 4
+    step = PagedKVCacheManager(L, 2, 16, max_blocks=256, block_size=B, device="cpu", dtype=torch.float32)
+    ref = PagedKVCacheManager(L, 2, 16, max_blocks=256, block_size=B, device="cpu", dtype=torch.float32)
+    for m in (step, ref):
+        a = m.allocate_sequence()
+        for l in range(L):
+            m.plan_append(a, l, 5 + l)  # different lengths per layer
+        m.fork_sequence(a)
+    got = step.plan_append_step([0, 1])
+    want = np.stack([ref.plan_append_batched([0, 1], l) for l in range(L)])
+    assert (got == want).all()
+    assert step.allocator.refcounts == ref.allocator.refcounts
