@@ -36,6 +36,7 @@ import time
 HERE = os.path.dirname(os.path.abspath(__file__))
 METRIC = "branch-decode tokens/sec on 1 GPU; paged-decode achieved HBM GB/s vs peak"
 PEAK_HBM_GBS = 8000.0
+PEAK_BF16_TFLOPS = 2500.0  # dense bf16 MFMA
 TRAFFIC_FILE = os.path.join(HERE, "profiles", "paged_decode_llama3_8b_traffic.txt")
 
 
@@ -339,6 +340,63 @@ def run_rows(args, dev) -> dict:
     return line
 
 
+def run_prefill(args, dev) -> dict:
+    import torch
+
+    from mentat_amd import ops
+
+    # Llama-3-8B attention shapes; one 2048-token prompt per sequence, batch 4.
+    B, S, Hq, Hkv, D = 4, 2048, 32, 8, 128
+    print("bench: building the prefill workload", file=sys.stderr, flush=True)
+    g = torch.Generator(device=dev).manual_seed(0)
+    sets = []
+    for _ in range(2):  # two input sets used in turn
+        q = torch.randn(B, S, Hq, D, generator=g, device=dev).to(torch.bfloat16)
+        k = torch.randn(B, S, Hkv, D, generator=g, device=dev).to(torch.bfloat16)
+        v = torch.randn(B, S, Hkv, D, generator=g, device=dev).to(torch.bfloat16)
+        sets.append((q, k, v))
+    out = torch.empty_like(sets[0][0])
+    state = {"i": 0}
+
+    def step():
+        q, k, v = sets[state["i"] & 1]
+        ops.prefill_attention(q, k, v, out=out)
+        state["i"] += 1
+
+    ms = _time_steps(step, args.steps, args.warmup, dev)
+    # causal: every query position i multiplies i+1 keys, two products (QK^T, PV) of 2*D flops each
+    flops = 4.0 * B * Hq * D * (S * (S + 1) / 2)
+    tflops = flops / (ms * 1e-3) / 1e12
+    cpu = None
+    if not args.no_cpu_baseline:
+        from oracle.attention import reference_cpu_prefill
+
+        torch.set_num_threads(max(1, int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))))
+        q, k, v = (t[:1].cpu() for t in sets[0])  # one of the B prompts
+        reps, total = 0, 0.0
+        while total < args.cpu_seconds or reps < 1:
+            t0 = time.perf_counter()
+            reference_cpu_prefill(q, k, v)
+            total += time.perf_counter() - t0
+            reps += 1
+        per = total / reps
+        cpu = {"value": round(flops / B / per / 1e12, 4), "unit": "TFLOP/s", "cores": torch.get_num_threads(),
+               "kind": "port",
+               "sample": f"1 of the {B} prompts, {reps} repetitions ({total:.1f} s): GQA expand + causal SDPA, "
+                         f"bf16, torch CPU"}
+    config = {
+        "workload": "causal GQA prefill attention, Llama-3-8B attention shapes",
+        "batch": B, "seq_len": S, "q_heads": Hq, "kv_heads": Hkv, "head_dim": D, "window": None,
+        "flops_per_step": flops, "rotation": "2 input sets used in turn",
+    }
+    line = _line(args, 0.0, ms, config, cpu, None)
+    line.update({"value": round(tflops, 2), "unit": "TFLOP/s"})
+    line["roofline"] = {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                        "frac": round(tflops / PEAK_BF16_TFLOPS, 4), "traffic": None}
+    line["data"] = "synthetic (seeded N(0,1) Q/K/V)"
+    return line
+
+
 class _IdTokenizer:
     """Prompts are token ids; decoding joins ids (the rollout never needs text)."""
 
@@ -411,7 +469,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--workload", choices=("decode", "tree", "rows", "e2e"), default="decode")
+    ap.add_argument("--workload", choices=("decode", "tree", "rows", "e2e", "prefill"), default="decode")
     ap.add_argument("--e2e-new-tokens", type=int, default=512)
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="minimum host time spent on the CPU baseline")
@@ -429,7 +487,8 @@ def main() -> int:
 
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
-    run = {"decode": run_decode, "tree": run_tree, "rows": run_rows, "e2e": run_e2e}[args.workload]
+    run = {"decode": run_decode, "tree": run_tree, "rows": run_rows, "e2e": run_e2e,
+           "prefill": run_prefill}[args.workload]
     print(json.dumps(run(args, dev)), flush=True)
     return 0
 

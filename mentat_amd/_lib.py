@@ -63,6 +63,14 @@ SIGNATURES: dict[str, tuple] = {
             _c_void_p, _c_size, _c_void_p,  # workspace, workspace_bytes, stream
         ],
     ),
+    "mentat_prefill_attention": (
+        _c_int,
+        [
+            _c_void_p, _c_void_p, _c_void_p, _c_void_p,  # q, k, v, out
+            _c_int, _c_int, _c_int, _c_int, _c_int,  # batch, seqlen, Hq, Hkv, D
+            _c_int, _c_float, _c_int, _c_void_p,  # window, scale, dtype, stream
+        ],
+    ),
     "mentat_kv_append": (
         _c_int,
         [

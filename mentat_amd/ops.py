@@ -25,6 +25,7 @@ from ._lib import (
 
 __all__ = [
     "paged_decode",
+    "prefill_attention",
     "tree_decode",
     "kv_append",
     "page_copy",
@@ -173,6 +174,51 @@ def paged_decode(
         ptr(ws), nbytes, stream_handle(dev),
     )
     check(st, "mentat_paged_decode")
+    return out
+
+
+def prefill_attention(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    *,
+    window_size: Optional[int] = None,
+    scale: Optional[float] = None,
+    out: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """Causal (optionally sliding-window) GQA attention over a batch of prompts.
+
+    q [B, S, Hq, D], k/v [B, S, Hkv, D] (bf16 or f16, D in {64, 128},
+    Hq/Hkv in {1, 2, 4, 8, 16}); position i attends to keys
+    max(0, i - window_size + 1) .. i (all of 0 .. i when window_size is None
+    or >= S), softmax scale D^-1/2 by default. Returns [B, S, Hq, D].
+    """
+    _require(q.dim() == 4 and k.dim() == 4 and v.dim() == 4, "q, k, v must be [B, S, H, D]")
+    B, S, Hq, D = q.shape
+    _require(k.shape == v.shape and k.shape[0] == B and k.shape[1] == S and k.shape[3] == D,
+             f"k/v shape {tuple(k.shape)} does not match q {tuple(q.shape)}")
+    Hkv = k.shape[2]
+    dev = q.device
+    _require(dev.type == "cuda", "prefill_attention runs on the GPU only (q is on the CPU)")
+    _require(q.dtype in (torch.bfloat16, torch.float16), f"prefill_attention needs bf16/f16, got {q.dtype}")
+    _require(k.dtype == q.dtype and v.dtype == q.dtype, "q/k/v dtypes differ")
+    _require(k.device == dev and v.device == dev, "q/k/v devices differ")
+    _require(D in (64, 128), f"head_dim {D} not supported (64, 128)")
+    _require(Hq % Hkv == 0 and Hq // Hkv in (1, 2, 4, 8, 16), f"Hq/Hkv = {Hq}/{Hkv} not supported")
+    q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
+    if out is None:
+        out = torch.empty_like(q)
+    else:
+        _require(out.shape == q.shape and out.dtype == q.dtype and out.is_contiguous(), "bad out")
+    if B == 0 or S == 0:
+        return out
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    window = 0 if window_size is None else int(window_size)
+    _require(window_size is None or window > 0, "window_size must be positive")
+    st = get_lib().mentat_prefill_attention(ptr(q), ptr(k), ptr(v), ptr(out), B, S, Hq, Hkv, D, window,
+                                            float(scale), DTYPE_CODES[q.dtype], stream_handle(dev))
+    check(st, "mentat_prefill_attention")
     return out
 
 

@@ -130,3 +130,27 @@ def reference_cpu_decode(q, k_pool, v_pool, page_tables, num_tokens, block_size)
         oi = F.scaled_dot_product_attention(qi, ki, vi, is_causal=False)
         outs.append(oi.squeeze(0).squeeze(1))
     return torch.stack(outs, dim=0)
+
+
+def reference_cpu_prefill(q, k, v, window_size=None):
+    """The reference's SDPA prefill path in torch on the CPU, in the model dtype
+    (adapters/attention_backend.py:43-96): transpose to (B, H, S, D), expand the
+    kv heads to the query heads (GQA), causal SDPA, or an explicit
+    sliding-window mask when window_size < S. Used as the timed CPU baseline of
+    the prefill kernel; the kernel's parity tests use a float64 restatement."""
+    import torch
+    import torch.nn.functional as F
+
+    q, k, v = q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2)
+    Hq, Hkv, S = q.size(1), k.size(1), q.size(2)
+    if Hkv != Hq:
+        g = Hq // Hkv
+        k = k.unsqueeze(2).expand(-1, -1, g, -1, -1).reshape(k.size(0), Hq, S, k.size(-1))
+        v = v.unsqueeze(2).expand(-1, -1, g, -1, -1).reshape(v.size(0), Hq, S, v.size(-1))
+    if window_size is not None and window_size < S:
+        i = torch.arange(S)
+        mask = (i[None, :] <= i[:, None]) & (i[None, :] >= (i[:, None] - window_size + 1))
+        o = F.scaled_dot_product_attention(q, k, v, attn_mask=mask)
+    else:
+        o = F.scaled_dot_product_attention(q, k, v, is_causal=True)
+    return o.transpose(1, 2)

@@ -102,3 +102,46 @@ def test_reference_cpu_path_matches_f64():
         tables, lens, B,
     ).numpy()
     np.testing.assert_allclose(o32, o64, rtol=1e-4, atol=1e-5)
+
+
+def test_reference_cpu_prefill_known_answers_and_masks():
+    """The CPU prefill baseline (the reference's SDPA path restated): one
+    position gives v; identical keys give the mean of V over each position's
+    window; and it agrees with explicit float64 masked softmax (GQA expand)."""
+    import math
+
+    import torch
+
+    from oracle.attention import reference_cpu_prefill
+
+    g = torch.Generator().manual_seed(0)
+    q = torch.randn(2, 1, 4, 16, generator=g, dtype=torch.float64)
+    k = torch.randn(2, 1, 2, 16, generator=g, dtype=torch.float64)
+    v = torch.randn(2, 1, 2, 16, generator=g, dtype=torch.float64)
+    assert torch.allclose(reference_cpu_prefill(q, k, v), v.repeat_interleave(2, dim=2))
+    S = 9
+    q = torch.randn(1, S, 2, 8, generator=g, dtype=torch.float64)
+    k = torch.randn(1, 1, 1, 8, generator=g, dtype=torch.float64).expand(1, S, 1, 8)
+    v = torch.randn(1, S, 1, 8, generator=g, dtype=torch.float64)
+    for w in (None, 3):
+        o = reference_cpu_prefill(q, k, v, window_size=w)
+        for i in range(S):
+            lo = 0 if w is None else max(0, i - w + 1)
+            assert torch.allclose(o[0, i, 0], v[0, lo:i + 1, 0].mean(0))
+            assert torch.allclose(o[0, i, 1], v[0, lo:i + 1, 0].mean(0))
+    B, S, Hq, Hkv, D = 2, 13, 6, 2, 8
+    q = torch.randn(B, S, Hq, D, generator=g, dtype=torch.float64)
+    k = torch.randn(B, S, Hkv, D, generator=g, dtype=torch.float64)
+    v = torch.randn(B, S, Hkv, D, generator=g, dtype=torch.float64)
+    for w in (None, 4, 13):
+        o = reference_cpu_prefill(q, k, v, window_size=w)
+        for h in range(Hq):
+            kh, vh = k[:, :, h // 3], v[:, :, h // 3]
+            s = torch.einsum("bid,bjd->bij", q[:, :, h], kh) / math.sqrt(D)
+            i = torch.arange(S)[:, None]
+            j = torch.arange(S)[None, :]
+            m = j <= i
+            if w is not None and w < S:
+                m &= j >= i - w + 1
+            want = torch.einsum("bij,bjd->bid", torch.softmax(s.masked_fill(~m, float("-inf")), -1), vh)
+            assert torch.allclose(o[:, :, h], want)
