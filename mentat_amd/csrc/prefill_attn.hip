@@ -7,16 +7,20 @@
 // scale 1/sqrt(D) unless given.
 //
 // A kv head's query rows are numbered r = position * G + g (g = head within
-// the group). A workgroup takes 64 consecutive rows of one (batch, kv head):
-// each of its 4 wavefronts owns 16 rows, which are the 16 columns of its MFMA
-// tiles (S^T = K.Q^T on v_mfma 16x16x32, online softmax in base 2 with a lazy
-// rescale, O += P.V on 16x16x16, as in the decode kernels). The workgroup
-// streams the 16-token K/V tiles its rows need through a two-stage LDS ring:
-// every thread issues one 16-byte load of K and one of V for the next tile
-// before the current tile is computed; V is written to LDS transposed (one
-// dim's 16 tokens per row), which is the P.V operand layout. Loads are
-// unconditional (the token index is clamped into the sequence) and values of
-// tokens past the sequence end are replaced by zeros.
+// the group). A workgroup takes kPfRows consecutive rows of one (batch, kv
+// head): each of its 4 wavefronts owns kPfCols 16-column MFMA tiles (S^T =
+// K.Q^T on v_mfma 16x16x32, online softmax in base 2 with a lazy rescale,
+// O += P.V, as in the decode kernels); tiles with no visible key in a step
+// skip it. The workgroup streams the kPfKeys-key K/V stages its rows need
+// through a two-stage LDS ring: every thread issues four 16-byte loads of K
+// and four of V (4 tokens x 8 dims) for the next stage before the current one
+// is computed, and writes V to LDS transposed (one dim's keys per row, 8 bytes
+// = 4 keys per write), which is the P.V operand layout. A stage is computed in
+// 32-key steps (two S^T chains, one softmax update, P.V on 16x16x32). Loads
+// are unconditional (the token index is clamped into the sequence) and values
+// of tokens past the sequence end are replaced by zeros. One tile per
+// wavefront and 32-key stages measured fastest (more tiles per wavefront
+// raise register use to one wavefront per SIMD).
 #include "mentat_common.h"
 
 namespace mentat {
@@ -66,15 +70,17 @@ struct PrefillParams {
 
 constexpr int kPfWaves = 4;
 constexpr int kPfThreads = 64 * kPfWaves;
-constexpr int kPfRows = 16 * kPfWaves;  // query rows per workgroup
+constexpr int kPfCols = 1;                         // 16-row column tiles per wavefront
+constexpr int kPfRows = 16 * kPfCols * kPfWaves;  // query rows per workgroup
 constexpr float kPfSlack = 8.f;
 
-// LDS stage: K rows (16 tokens, padded by 16 bytes) and V^T rows (one dim's 16
-// tokens, padded by 8): conflict-free 16-lane MFMA operand reads.
+// LDS stage of kPfKeys keys: K rows (one token, padded by 16 bytes) and V^T
+// rows (one dim's kPfKeys tokens, padded by 8 bytes).
+constexpr int kPfKeys = 32;
 template <int D> struct PfLds {
   static constexpr int KRS = 2 * D + 16;
-  static constexpr int VRS = 40;
-  static constexpr int KST = 16 * KRS;
+  static constexpr int VRS = 2 * kPfKeys + 8;
+  static constexpr int KST = kPfKeys * KRS;
   static constexpr int STAGE = KST + D * VRS;
 };
 
@@ -82,9 +88,10 @@ template <typename T, int D, int G>
 __global__ __launch_bounds__(kPfThreads) void prefill_attn_kernel(PrefillParams p) {
   using S = typename T::storage;
   using L = PfLds<D>;
-  constexpr int KS = D / 32, NT = D / 16;
+  constexpr int KS = D / 32, NT = D / 16, NC = kPfCols;
   constexpr int CH = D / 8;                 // 16-byte chunks per token row
-  static_assert(16 * CH <= kPfThreads, "one K and one V chunk per thread and tile");
+  constexpr int NQ = kPfKeys / 4;           // token quads per stage
+  static_assert(NQ * CH <= kPfThreads, "one (token quad, chunk) per thread and stage");
   __shared__ __attribute__((aligned(16))) char lds[2 * L::STAGE];
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -98,133 +105,197 @@ __global__ __launch_bounds__(kPfThreads) void prefill_attn_kernel(PrefillParams 
   const int pos_lo = r0 / G;
   const int pos_hi = min(p.S - 1, (r0 + kPfRows - 1) / G);
   const int key_lo = p.window > 0 ? max(0, pos_lo - p.window + 1) : 0;
-  const int t_lo = key_lo / 16, t_hi = pos_hi / 16;
+  const int t_lo = key_lo / kPfKeys, t_hi = pos_hi / kPfKeys;
 
-  // This wave's 16 rows (columns of its tiles): row rw + lr -> position, head.
-  const int rw = r0 + 16 * wave;
-  const int wpos_lo = min(rw / G, p.S - 1);
-  const int wpos_hi = min((rw + 15) / G, p.S - 1);
-  const bool wave_live = rw < rows;
-  const int row = rw + lr;
-  const bool col_ok = row < rows;
-  const int qpos = col_ok ? row / G : 0;
-  const int qhead = hk * G + (col_ok ? row % G : 0);
-  const int kmin = p.window > 0 ? qpos - p.window + 1 : 0;  // first key of this column
-
-  // Q^T operand: column lr holds Q[b, qpos, qhead, 32s + 8lg .. +8].
-  uint4 qo[KS];
-  {
-    const S* qp = (const S*)p.q + (((long)b * p.S + qpos) * p.Hq + qhead) * D + 8 * lg;
+  // Column tile c of this wave: rows rw + 16c + lr -> position, head.
+  const int rw = r0 + 16 * NC * wave;
+  int tpos_hi[NC], tkey_lo[NC];   // per tile (wave-uniform): last position, first key
+  int qpos[NC], kmin[NC];         // per lane's column
+  bool col_ok[NC];
+  uint4 qo[NC][KS];
+  f32x4_t o[NC][NT];
+  float m[NC], l[NC];
+  static_for<NC>([&](auto c_) {
+    constexpr int c = decltype(c_)::value;
+    const int rt = rw + 16 * c;
+    tpos_hi[c] = rt < rows ? min((rt + 15) / G, p.S - 1) : -1;
+    tkey_lo[c] = p.window > 0 ? min(rt / G, p.S - 1) - p.window + 1 : 0;
+    const int row = rt + lr;
+    col_ok[c] = row < rows;
+    qpos[c] = col_ok[c] ? row / G : 0;
+    kmin[c] = p.window > 0 ? qpos[c] - p.window + 1 : 0;
+    const int qhead = hk * G + (col_ok[c] ? row % G : 0);
+    const S* qp = (const S*)p.q + (((long)b * p.S + qpos[c]) * p.Hq + qhead) * D + 8 * lg;
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
       const uint4 w = *(const uint4*)(qp + 32 * s);
-      qo[s] = col_ok ? w : make_uint4(0, 0, 0, 0);
+      qo[c][s] = col_ok[c] ? w : make_uint4(0, 0, 0, 0);
     }
-  }
-  float m = kNegInf, l = 0.f;
-  f32x4_t o[NT];
+    m[c] = kNegInf;
+    l[c] = 0.f;
 #pragma unroll
-  for (int j = 0; j < NT; ++j) o[j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < NT; ++j) o[c][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  });
 
-  // Staging: thread tid < 16*CH moves chunk (token tid / CH, dims 8*(tid % CH) ..+8);
-  // the other threads load a copy of the last chunk and store nothing, so every
-  // load is issued outside any branch.
-  const bool loader = tid < 16 * CH;
-  const int lid = min(tid, 16 * CH - 1);
-  const int ltok = lid / CH, lch = lid - (lid / CH) * CH;
-  auto gload = [&](int t, uint4& kw, uint4& vw) {
-    const int tok = t * 16 + ltok;
-    const int tc = min(tok, p.S - 1);
-    const long off = (((long)b * p.S + tc) * p.Hkv + hk) * D + 8 * lch;
-    kw = *(const uint4*)((const S*)p.k + off);
-    vw = *(const uint4*)((const S*)p.v + off);
-    if (tok >= p.S) { kw = make_uint4(0, 0, 0, 0); vw = make_uint4(0, 0, 0, 0); }
+  // Staging: thread tid < NQ*CH moves tokens 4*tq .. 4*tq+3, dims 8*lc .. 8*lc+7 of
+  // K and V; the other threads load a copy of the last block and store nothing,
+  // so every load is issued outside any branch.
+  const bool loader = tid < NQ * CH;
+  const int lid = min(tid, NQ * CH - 1);
+  const int tq = lid / CH, lc = lid - (lid / CH) * CH;
+  uint4 kw[4], vw[4];
+  auto gload = [&](int t) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int tok = t * kPfKeys + 4 * tq + u;
+      const int tc = min(tok, p.S - 1);
+      const long off = (((long)b * p.S + tc) * p.Hkv + hk) * D + 8 * lc;
+      kw[u] = *(const uint4*)((const S*)p.k + off);
+      vw[u] = *(const uint4*)((const S*)p.v + off);
+      if (tok >= p.S) { kw[u] = make_uint4(0, 0, 0, 0); vw[u] = make_uint4(0, 0, 0, 0); }
+    }
   };
-  auto lstore = [&](int stage, const uint4& kw, const uint4& vw) {
+  auto lstore = [&](int stage) {
     char* st = lds + stage * L::STAGE;
-    *(uint4*)(st + ltok * L::KRS + lch * 16) = kw;
-    const uint16_t* e = (const uint16_t*)&vw;
-    char* vt = st + L::KST;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) *(uint16_t*)(vt + (8 * lch + i) * L::VRS + 2 * ltok) = e[i];
+    for (int u = 0; u < 4; ++u) *(uint4*)(st + (4 * tq + u) * L::KRS + lc * 16) = kw[u];
+    // V^T row 8lc + i gets tokens 4tq .. 4tq+3 of dim 8lc + i: one 8-byte write.
+    const uint32_t* w0 = (const uint32_t*)&vw[0];
+    const uint32_t* w1 = (const uint32_t*)&vw[1];
+    const uint32_t* w2 = (const uint32_t*)&vw[2];
+    const uint32_t* w3 = (const uint32_t*)&vw[3];
+    char* vt = st + L::KST + 8 * tq;
+#pragma unroll
+    for (int h = 0; h < 4; ++h) {
+      // dims 8lc + 2h (low halves) and 8lc + 2h + 1 (high halves)
+      const uint2 lo = make_uint2(__builtin_amdgcn_perm(w1[h], w0[h], 0x05040100u),
+                                  __builtin_amdgcn_perm(w3[h], w2[h], 0x05040100u));
+      const uint2 hi = make_uint2(__builtin_amdgcn_perm(w1[h], w0[h], 0x07060302u),
+                                  __builtin_amdgcn_perm(w3[h], w2[h], 0x07060302u));
+      *(uint2*)(vt + (8 * lc + 2 * h) * L::VRS) = lo;
+      *(uint2*)(vt + (8 * lc + 2 * h + 1) * L::VRS) = hi;
+    }
   };
 
-  uint4 kw, vw;
-  gload(t_lo, kw, vw);
-  if (loader) lstore(0, kw, vw);
+  gload(t_lo);
+  if (loader) lstore(0);
   __syncthreads();
   for (int t = t_lo; t <= t_hi; ++t) {
     const int stage = (t - t_lo) & 1;
     const bool more = t < t_hi;
-    gload(min(t + 1, t_hi), kw, vw);  // the last iteration reloads its own tile and stores nothing
-    // Tiles wholly after this wave's last position or before its first key are skipped.
-    const bool use = wave_live && 16 * t <= wpos_hi &&
-                     (p.window <= 0 || 16 * t + 15 >= wpos_lo - p.window + 1);
-    if (use) {
-      const char* st = lds + stage * L::STAGE;
-      uint4 kr[KS];
-      uint2 vr[NT];
+    gload(min(t + 1, t_hi));  // the last iteration reloads its own stage and stores nothing
+    const char* st = lds + stage * L::STAGE;
+    // Two 32-key steps: per column tile two S^T chains, one softmax update and
+    // O += P.V on 16x16x32 (k = 8lg + i <-> key 4lg + i of the first 16 keys for
+    // i < 4, of the second 16 for i >= 4). Each K/V operand read from LDS feeds
+    // the MFMAs of every live column tile.
 #pragma unroll
-      for (int s = 0; s < KS; ++s) kr[s] = *(const uint4*)(st + lr * L::KRS + (32 * s + 8 * lg) * 2);
+    for (int h2 = 0; h2 < kPfKeys / 32; ++h2) {
+      const int kb = t * kPfKeys + 32 * h2;  // first key of this step
+      bool live[NC];
+      bool any = false;
+      static_for<NC>([&](auto c_) {
+        constexpr int c = decltype(c_)::value;
+        live[c] = kb <= tpos_hi[c] && kb + 31 >= tkey_lo[c];
+        any |= live[c];
+      });
+      if (!any) continue;
+      const char* ks = st + (32 * h2) * L::KRS;
+      f32x4_t s0[NC], s1[NC];
+      static_for<NC>([&](auto c_) {
+        constexpr int c = decltype(c_)::value;
+        s0[c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        s1[c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      });
 #pragma unroll
-      for (int j = 0; j < NT; ++j) vr[j] = *(const uint2*)(st + L::KST + (16 * j + lr) * L::VRS + 8 * lg);
-      f32x4_t sacc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int s = 0; s < KS; ++s) sacc = PMfma<T>::qk(kr[s], qo[s], sacc);
-      const int key0 = t * 16 + 4 * lg;
-      float sc[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int kk = key0 + i;
-        sc[i] = sacc[i] * p.scale_log2;
-        if (!col_ok || kk > qpos || kk < kmin) sc[i] = kNegInf;
+      for (int s = 0; s < KS; ++s) {
+        const uint4 k0 = *(const uint4*)(ks + lr * L::KRS + (32 * s + 8 * lg) * 2);
+        const uint4 k1 = *(const uint4*)(ks + (16 + lr) * L::KRS + (32 * s + 8 * lg) * 2);
+        static_for<NC>([&](auto c_) {
+          constexpr int c = decltype(c_)::value;
+          if (live[c]) {
+            s0[c] = PMfma<T>::qk(k0, qo[c][s], s0[c]);
+            s1[c] = PMfma<T>::qk(k1, qo[c][s], s1[c]);
+          }
+        });
       }
-      float pm = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
-      const bool grow = (m == kNegInf) ? (pm != kNegInf) : (pm > m + kPfSlack);
-      if (__builtin_amdgcn_ballot_w64(grow)) {
-        pm = fmaxf(pm, __shfl_xor(pm, 16));
-        pm = fmaxf(pm, __shfl_xor(pm, 32));
-        const float mn = fmaxf(m, pm);
-        const float alpha = (mn == kNegInf) ? 1.f : fast_exp2(m - mn);
-        l *= alpha;
-        m = mn;
+      uint4 pk[NC];
+      static_for<NC>([&](auto c_) {
+        constexpr int c = decltype(c_)::value;
+        if (!live[c]) return;
+        float sc[8];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const float ar = __shfl(alpha, 4 * lg + i);
-#pragma unroll
-          for (int j = 0; j < NT; ++j) o[j][i] *= ar;
+          const int ka = kb + 4 * lg + i, kc = ka + 16;
+          sc[i] = s0[c][i] * p.scale_log2;
+          sc[4 + i] = s1[c][i] * p.scale_log2;
+          if (!col_ok[c] || ka > qpos[c] || ka < kmin[c]) sc[i] = kNegInf;
+          if (!col_ok[c] || kc > qpos[c] || kc < kmin[c]) sc[4 + i] = kNegInf;
         }
+        float pm = fmaxf(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])),
+                         fmaxf(fmaxf(sc[4], sc[5]), fmaxf(sc[6], sc[7])));
+        const bool grow = (m[c] == kNegInf) ? (pm != kNegInf) : (pm > m[c] + kPfSlack);
+        if (__builtin_amdgcn_ballot_w64(grow)) {
+          pm = fmaxf(pm, __shfl_xor(pm, 16));
+          pm = fmaxf(pm, __shfl_xor(pm, 32));
+          const float mn = fmaxf(m[c], pm);
+          const float alpha = (mn == kNegInf) ? 1.f : fast_exp2(m[c] - mn);
+          l[c] *= alpha;
+          m[c] = mn;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float ar = __shfl(alpha, 4 * lg + i);
+#pragma unroll
+            for (int j = 0; j < NT; ++j) o[c][j][i] *= ar;
+          }
+        }
+        const float ms = (m[c] == kNegInf) ? 0.f : m[c];
+        f32x4_t pa, pb;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          pa[i] = fast_exp2(sc[i] - ms);
+          pb[i] = fast_exp2(sc[4 + i] - ms);
+        }
+        l[c] += ((pa[0] + pa[1]) + (pa[2] + pa[3])) + ((pb[0] + pb[1]) + (pb[2] + pb[3]));
+        const uint2 ua = PMfma<T>::pack(pa), ub = PMfma<T>::pack(pb);
+        pk[c] = make_uint4(ua.x, ua.y, ub.x, ub.y);
+      });
+      const char* vs = st + L::KST + (32 * h2 + 4 * lg) * 2;
+#pragma unroll
+      for (int j = 0; j < NT; ++j) {
+        const uint2 va = *(const uint2*)(vs + (16 * j + lr) * L::VRS);
+        const uint2 vb = *(const uint2*)(vs + (16 * j + lr) * L::VRS + 32);
+        const uint4 vv = make_uint4(va.x, va.y, vb.x, vb.y);
+        static_for<NC>([&](auto c_) {
+          constexpr int c = decltype(c_)::value;
+          if (live[c]) o[c][j] = PMfma<T>::qk(pk[c], vv, o[c][j]);
+        });
       }
-      const float ms = (m == kNegInf) ? 0.f : m;
-      f32x4_t pr;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) pr[i] = fast_exp2(sc[i] - ms);
-      l += (pr[0] + pr[1]) + (pr[2] + pr[3]);
-      const uint2 pa = PMfma<T>::pack(pr);
-#pragma unroll
-      for (int j = 0; j < NT; ++j) o[j] = PMfma<T>::pv(pa, vr[j], o[j]);
     }
-    if (loader && more) lstore(stage ^ 1, kw, vw);
+    if (loader && more) lstore(stage ^ 1);
     __syncthreads();
   }
 
-  if (!wave_live) return;
-  l += __shfl_xor(l, 16);
-  l += __shfl_xor(l, 32);
-  // O rows are the wave's columns 4lg + i; their l sits in lane 4lg + i.
+  // O rows of tile c are its columns 4lg + i; their l sits in lane 4lg + i.
+  static_for<NC>([&](auto c_) {
+    constexpr int c = decltype(c_)::value;
+    float lt = l[c];
+    lt += __shfl_xor(lt, 16);
+    lt += __shfl_xor(lt, 32);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int c = 4 * lg + i;
-    const float lc = __shfl(l, c);
-    const int r = rw + c;
-    if (r < rows) {
-      const int pos = r / G, head = hk * G + r % G;
-      const float inv = lc > 0.f ? 1.f / lc : 0.f;
-      const long ob = (((long)b * p.S + pos) * p.Hq + head) * D + lr;
+    for (int i = 0; i < 4; ++i) {
+      const int col = 4 * lg + i;
+      const float lcol = __shfl(lt, col);
+      const int r = rw + 16 * c + col;
+      if (r < rows) {
+        const int pos = r / G, head = hk * G + r % G;
+        const float inv = lcol > 0.f ? 1.f / lcol : 0.f;
+        const long ob = (((long)b * p.S + pos) * p.Hq + head) * D + lr;
 #pragma unroll
-      for (int j = 0; j < NT; ++j) Elem<T>::store1(p.out, ob + 16 * j, o[j][i] * inv);
+        for (int j = 0; j < NT; ++j) Elem<T>::store1(p.out, ob + 16 * j, o[c][j][i] * inv);
+      }
     }
-  }
+  });
 }
 
 template <typename T, int D, int G>
