@@ -160,6 +160,33 @@ int mentat_prefill_attention(const void* q, const void* k, const void* v, void* 
                              int Hq, int Hkv, int D, int window, float scale, int dtype, void* stream);
 
 /* ------------------------------------------------------------------------
+ * Semantic-diversity prune.
+ *
+ * mentat_semantic_ema replaces core/generator.py:376-398
+ * (_update_semantic_vectors): for each of n leaves, row i of `hidden`
+ * ([n, hidden_stride], H used) is written to the H-element vector at
+ * dst_ptrs[i] when init[i] != 0 (a new leaf clones its hidden state), and
+ * otherwise folded in as v.mul_(mul_scale).add_(h, alpha=add_scale) with the
+ * rounding of torch's kernels: rnd(fma(add_scale, h, rnd(v * mul_scale))).
+ * dst_ptrs, init: device arrays of n entries. Vectors in `dtype`.
+ *
+ * mentat_semantic_similar replaces the similarity mask of
+ * core/generator.py:400-460 (_prune_similar): for M candidate vectors at
+ * ptrs[i], mask[i*M + j] = 1 iff i < j, group[i] == group[j],
+ * parent_key[i] != parent_key[j] (siblings are never compared) and
+ * rnd(dot(n_i, n_j)) > rnd(threshold), where n_i = F.normalize(v_i, p=2) in
+ * the vectors' dtype (float norm rounded, clamp_min(1e-12), float divide
+ * rounded) and rnd rounds to that dtype, as torch's comparison with a scalar
+ * does. scratch: at least M*H elements of the dtype. mask: M*M bytes.
+ * ---------------------------------------------------------------------- */
+int mentat_semantic_ema(const int64_t* dst_ptrs, const void* hidden, const int32_t* init, int n, int H,
+                        int64_t hidden_stride, float mul_scale, float add_scale, int dtype, void* stream);
+
+int mentat_semantic_similar(const int64_t* ptrs, const int32_t* parent_key, const int32_t* group, int M, int H,
+                            float threshold, int dtype, void* scratch, size_t scratch_bytes, uint8_t* mask,
+                            void* stream);
+
+/* ------------------------------------------------------------------------
  * KV append: write n new token rows into the pools, fused with the lazy
  * copy-on-write of a shared tail page and the device block-table update.
  *

@@ -71,6 +71,20 @@ SIGNATURES: dict[str, tuple] = {
             _c_int, _c_float, _c_int, _c_void_p,  # window, scale, dtype, stream
         ],
     ),
+    "mentat_semantic_ema": (
+        _c_int,
+        [
+            _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int,  # dst_ptrs, hidden, init, n, H
+            _c_i64, _c_float, _c_float, _c_int, _c_void_p,  # hidden_stride, mul_scale, add_scale, dtype, stream
+        ],
+    ),
+    "mentat_semantic_similar": (
+        _c_int,
+        [
+            _c_void_p, _c_void_p, _c_void_p, _c_int, _c_int,  # ptrs, parent_key, group, M, H
+            _c_float, _c_int, _c_void_p, _c_size, _c_void_p, _c_void_p,  # thr, dtype, scratch, bytes, mask, stream
+        ],
+    ),
     "mentat_kv_append": (
         _c_int,
         [

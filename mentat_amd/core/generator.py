@@ -29,7 +29,6 @@ from typing import Optional
 
 import numpy as np
 import torch
-import torch.nn.functional as F
 
 from .. import ops
 from ..adapters.adapter_factory import ModelAdapter, get_adapter
@@ -289,13 +288,28 @@ class MentatGenerator:
 
     # ---- semantic diversity (reference :376-497) ----------------------------------------
     def _update_semantic_vectors(self, leaves: list[TreeNode], hidden_states: torch.Tensor) -> None:
-        a = self.ema_alpha
-        for i, leaf in enumerate(leaves):
-            h = hidden_states[i]
-            if leaf.semantic_vector is None:
-                leaf.semantic_vector = h.clone()
-            else:
-                leaf.semantic_vector.mul_(1.0 - a).add_(h, alpha=a)
+        """EMA of every leaf's semantic vector (reference :376-398) in one launch
+        (ops.semantic_ema): a new leaf takes its hidden state (as h.clone()),
+        the others v.mul_(1 - alpha).add_(h, alpha=alpha) with torch's rounding.
+        New leaves' vectors are rows of one fresh buffer."""
+        if not leaves:
+            return
+        fresh = [leaf.semantic_vector is None for leaf in leaves]
+        n_new = sum(fresh)
+        if n_new:
+            buf = torch.empty(n_new, hidden_states.shape[1], dtype=hidden_states.dtype, device=hidden_states.device)
+            k = 0
+            for leaf, f in zip(leaves, fresh):
+                if f:
+                    leaf.semantic_vector = buf[k]
+                    k += 1
+        vecs = []
+        for leaf in leaves:
+            v = leaf.semantic_vector
+            if not v.is_contiguous() or v.dtype != hidden_states.dtype:
+                v = leaf.semantic_vector = v.to(hidden_states.dtype).contiguous()
+            vecs.append(v)
+        ops.semantic_ema(vecs, hidden_states.contiguous(), fresh, self.ema_alpha)
 
     def _prune_similar(self, tree: PrefixTree, step: int, log=None) -> None:
         log = self if log is None else log
@@ -334,19 +348,19 @@ class MentatGenerator:
     def _similar_pairs(self, sv_leaves: list[TreeNode], groups: list) -> list:
         """(i, j), i < j, row-major: leaves of the same group (tree) whose semantic
         vectors have cosine similarity above the threshold and that are not
-        siblings (reference :447-460; the mask is built on the host in one go)."""
-        M = len(sv_leaves)
-        sv = torch.stack([l.semantic_vector for l in sv_leaves], dim=0)
-        normed = F.normalize(sv, p=2, dim=1)
-        sim = torch.mm(normed, normed.t().contiguous())
-        par = np.array([id(l.parent) if l.parent is not None else -1 - i for i, l in enumerate(sv_leaves)])
-        grp = np.asarray(groups)
-        keep = np.triu(np.ones((M, M), dtype=bool), k=1)
-        keep &= par[:, None] != par[None, :]
-        keep &= grp[:, None] == grp[None, :]
-        mask = torch.from_numpy(keep).to(sim.device)
-        sim = sim * mask
-        return (sim > self.semantic_similarity_threshold).nonzero(as_tuple=False).tolist()
+        siblings (reference :447-460). The mask is one device call
+        (ops.semantic_similar_mask: F.normalize + product in the vectors' dtype,
+        triangle, sibling and group masks) read back as M*M bytes."""
+        keys, parents = [], {}
+        for i, leaf in enumerate(sv_leaves):
+            if leaf.parent is None:
+                keys.append(-1 - i)  # never equal to another leaf's key
+            else:
+                keys.append(parents.setdefault(id(leaf.parent), len(parents)))
+        mask = ops.semantic_similar_mask([l.semantic_vector for l in sv_leaves], keys, groups,
+                                         self.semantic_similarity_threshold)
+        ii, jj = np.nonzero(mask)
+        return list(zip(ii.tolist(), jj.tolist()))
 
     # ------------------------------------------------------------------
     def get_diagnostics(self) -> dict:

@@ -10,6 +10,7 @@ import math
 from dataclasses import dataclass
 from typing import Optional
 
+import numpy as np
 import torch
 
 from ._lib import (
@@ -26,6 +27,8 @@ from ._lib import (
 __all__ = [
     "paged_decode",
     "prefill_attention",
+    "semantic_ema",
+    "semantic_similar_mask",
     "tree_decode",
     "kv_append",
     "page_copy",
@@ -220,6 +223,56 @@ def prefill_attention(
                                             float(scale), DTYPE_CODES[q.dtype], stream_handle(dev))
     check(st, "mentat_prefill_attention")
     return out
+
+
+def semantic_ema(vectors: list, hidden: torch.Tensor, fresh: list, alpha: float) -> None:
+    """Fold row i of ``hidden`` [n, H] into ``vectors[i]`` (an H-element
+    contiguous tensor on the same device, updated in place): copied when
+    ``fresh[i]``, else ``v.mul_(1 - alpha).add_(h, alpha=alpha)`` with torch's
+    rounding. One launch for all rows."""
+    n = len(vectors)
+    if n == 0:
+        return
+    _require(hidden.dim() == 2 and hidden.shape[0] == n and hidden.stride(1) == 1, "hidden must be [n, H], rows dense")
+    _require(hidden.dtype in DTYPE_CODES, f"unsupported dtype {hidden.dtype}")
+    dev, H = hidden.device, hidden.shape[1]
+    _require(dev.type == "cuda", "semantic_ema runs on the GPU only")
+    for v in vectors:
+        _require(v.dtype == hidden.dtype and v.device == dev and v.is_contiguous() and v.numel() == H,
+                 "every vector must be a contiguous H-element tensor of hidden's dtype and device")
+    meta = torch.tensor([v.data_ptr() for v in vectors] + [int(bool(f)) for f in fresh], dtype=torch.int64)
+    meta = meta.to(dev)
+    init = meta[n:].to(torch.int32)
+    st = get_lib().mentat_semantic_ema(ptr(meta), ptr(hidden), ptr(init), n, H, hidden.stride(0),
+                                       float(np.float32(1.0 - alpha)), float(np.float32(alpha)),
+                                       DTYPE_CODES[hidden.dtype], stream_handle(dev))
+    check(st, "mentat_semantic_ema")
+
+
+def semantic_similar_mask(vectors: list, parent_key: list, group: list, threshold: float) -> np.ndarray:
+    """Host bool [M, M]: entry (i, j) is set iff i < j, same group, different
+    parent key, and the cosine similarity of the two vectors (F.normalize +
+    mm in their dtype) exceeds ``threshold``."""
+    M = len(vectors)
+    if M == 0:
+        return np.zeros((0, 0), dtype=bool)
+    dev, dt = vectors[0].device, vectors[0].dtype
+    H = vectors[0].numel()
+    _require(dev.type == "cuda", "semantic_similar_mask runs on the GPU only")
+    _require(dt in DTYPE_CODES, f"unsupported dtype {dt}")
+    for v in vectors:
+        _require(v.dtype == dt and v.device == dev and v.is_contiguous() and v.numel() == H,
+                 "vectors must be contiguous, of one dtype, device and length")
+    meta = torch.tensor([v.data_ptr() for v in vectors] + [int(k) for k in parent_key] + [int(g) for g in group],
+                        dtype=torch.int64).to(dev)
+    keys = meta[M:].to(torch.int32)
+    scratch = torch.empty(M * H, dtype=dt, device=dev)
+    mask = torch.empty(M * M, dtype=torch.uint8, device=dev)
+    st = get_lib().mentat_semantic_similar(ptr(meta), ptr(keys[:M]), ptr(keys[M:]), M, H, float(threshold),
+                                           DTYPE_CODES[dt], ptr(scratch), scratch.numel() * scratch.element_size(),
+                                           ptr(mask), stream_handle(dev))
+    check(st, "mentat_semantic_similar")
+    return mask.cpu().numpy().reshape(M, M).astype(bool)
 
 
 def kv_append(
