@@ -407,6 +407,44 @@ class _IdTokenizer:
         return " ".join(str(i) for i in ids)
 
 
+def _cpu_baseline_e2e(model, prompt, new_tokens: int, knobs: dict, seconds: float) -> dict:
+    """The reference's rollout restated on the host cores (oracle.rollout_cpu):
+    one prompt (the reference runs prompts one after another), the same weights
+    copied to the CPU, decode stopped after `seconds`."""
+    import torch
+
+    from oracle.rollout_cpu import reference_cpu_rollout
+
+    torch.set_num_threads(max(1, int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))))
+    print("bench: copying the weights to the host for the CPU baseline", file=sys.stderr, flush=True)
+    prev = torch.get_default_dtype()
+    torch.set_default_dtype(next(model.parameters()).dtype)
+    try:
+        with torch.device("meta"):
+            cpu_model = type(model)(model.config)
+    finally:
+        torch.set_default_dtype(prev)
+    cpu_model = cpu_model.to_empty(device="cpu")
+    with torch.no_grad():
+        for (_, pc), (_, pg) in zip(cpu_model.named_parameters(), model.named_parameters()):
+            pc.copy_(pg)
+        for (_, bc), (_, bg) in zip(cpu_model.named_buffers(), model.named_buffers()):
+            bc.copy_(bg)
+    cpu_model.eval()
+    r = reference_cpu_rollout(cpu_model, prompt, max_new_tokens=new_tokens, time_budget_s=seconds,
+                              max_active_branches=knobs["max_active_branches"],
+                              branching_factor=knobs["branching_factor"],
+                              entropy_threshold=knobs["entropy_threshold"], eos_token_id=128001,
+                              block_size=knobs["block_size"])
+    del cpu_model
+    tps = r["decode_tokens"] / r["decode_s"] if r["decode_s"] > 0 else 0.0
+    return {"value": round(tps, 3), "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"1 prompt x {r['steps']} decode steps ({r['decode_tokens']} branch tokens, "
+                      f"{r['decode_s']:.1f} s; live leaves {r['trace'][:8]}...): the reference's rollout restated in "
+                      f"torch on the host (gather + per-sequence SDPA per layer), bf16; the reference runs "
+                      f"prompts one after another, so this rate is also its whole-job rate"}
+
+
 def run_e2e(args, dev) -> dict:
     import numpy as np
     import torch
@@ -454,7 +492,10 @@ def run_e2e(args, dev) -> dict:
         "results": sum(len(r) for r in results), "kv_blocks_peak": d["kv_blocks_peak"],
         "weight_bytes": wbytes,
     }
-    line = _line(args, 0.0, ms, config, None, None)
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = _cpu_baseline_e2e(model, prompts[0], new_tokens, knobs, args.cpu_seconds)
+    line = _line(args, 0.0, ms, config, cpu, None)
     line.update({"metric": METRIC, "value": round(d["decode_throughput_tps"], 1), "unit": "tokens/s"})
     # per-step HBM floor: the weights once per step
     line["roofline"] = {"bound": "hbm", "achieved": round(wbytes / (ms * 1e-3) / 1e9, 1), "peak": PEAK_HBM_GBS,

@@ -27,8 +27,18 @@ K/V stores, of its own input buffer and of the paged-decode workspace, so
     bucket before the first capture, and this object keeps it alive.
 Warm-up and capture run with an all-padding input, which writes nothing to
 the cache.
+
+No object is destroyed while a capture is active: the garbage collector runs
+just before each capture and stays disabled during it. (A finished run's
+graphs, pools and pinned buffers, if left to the cyclic collector, could
+otherwise be torn down in the middle of another capture, where the HIP calls
+of that teardown are not allowed and abort the process.) This object also
+holds no reference back to its wrapper, so a dropped generator's graphs are
+freed by reference counting, outside any capture.
 """
 from __future__ import annotations
+
+import gc
 
 import numpy as np
 import torch
@@ -50,7 +60,6 @@ class DecodeGraphs:
     """Captured batched decode forwards for one PagedModelWrapper."""
 
     def __init__(self, wrapper, buckets=BUCKETS):
-        self.w = wrapper
         self.a = wrapper.adapter
         self.m = wrapper.kv_cache_mgr
         self.dev = wrapper.device
@@ -157,8 +166,15 @@ class DecodeGraphs:
                 self._forward(b.dev, nb)
         torch.cuda.current_stream(self.dev).wait_stream(s)
         g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g, stream=s):
-            b.logits, b.hidden = self._forward(b.dev, nb)
+        gc_on = gc.isenabled()
+        gc.collect()
+        gc.disable()
+        try:
+            with torch.cuda.graph(g, stream=s):
+                b.logits, b.hidden = self._forward(b.dev, nb)
+        finally:
+            if gc_on:
+                gc.enable()
         torch.cuda.current_stream(self.dev).wait_stream(s)
         b.graph = g
         b.version = m.tables_version

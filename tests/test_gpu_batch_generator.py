@@ -60,3 +60,25 @@ def test_batched_rollouts_match_single_prompt_rollouts(gpu, gate, thr):
     single_max = max(max(d["active_branch_trace"] or [1]) for _, d in singles)
     assert max(bg.batch_trace) > single_max
     assert diag["decode_tokens_total"] == sum(sum(d["active_branch_trace"]) for _, d in singles)
+
+
+def test_cpu_rollout_restatement_follows_the_generator(gpu):
+    """The CPU baseline's restatement (oracle.rollout_cpu) against the product
+    generator on the fp32 plumbing model, absolute gate: the same live-leaf trace
+    and the same sequences."""
+    import make_cfg1_trajectory as mk
+    from mentat_amd.core.generator import MentatGenerator
+    from oracle.rollout_cpu import reference_cpu_rollout
+
+    print("case cpu rollout restatement vs generator", flush=True)
+    model = mk.build_model()
+    ids = _prompts()[1]
+    knobs = dict(max_active_branches=6, branching_factor=3, entropy_threshold=2.0)
+    r = reference_cpu_rollout(model, ids, max_new_tokens=20, time_budget_s=1e9, block_size=16, max_blocks=4096,
+                              **knobs)
+    with torch.no_grad():
+        g = MentatGenerator(model.to("cuda"), mk.StubTokenizer(ids), gate="absolute", max_new_tokens=20,
+                            block_size=16, max_blocks=4096, **knobs)
+        g.generate("stub")
+    assert r["trace"] == g.get_diagnostics()["active_branch_trace"]
+    assert r["decode_tokens"] == sum(r["trace"])

@@ -140,3 +140,41 @@ def test_rollouts_with_and_without_capture(gpu, gate, thr):
         assert d0["prompts"][p]["active_branch_trace"] == d1["prompts"][p]["active_branch_trace"]
         assert [x[::2] for x in d0["prompts"][p]["branch_points"]] == \
             [x[::2] for x in d1["prompts"][p]["branch_points"]]
+
+
+def test_no_garbage_collection_during_capture(gpu):
+    """Captures run with the garbage collector off (collected just before):
+    a dropped wrapper's graphs are never torn down inside another capture.
+    The forward is spied on; whenever the stream is capturing, gc must be off,
+    and gc's state is restored afterwards."""
+    import gc
+
+    from mentat_amd.core import graph_decode
+
+    print("case gc state during capture", flush=True)
+    model = _bf16_model()
+    seen = []
+    orig = graph_decode.DecodeGraphs._forward
+
+    def spy(self, buf, nb):
+        seen.append((torch.cuda.is_current_stream_capturing(), gc.isenabled()))
+        return orig(self, buf, nb)
+
+    graph_decode.DecodeGraphs._forward = spy
+    try:
+        with torch.no_grad():
+            w0 = _wrapper(model, True)
+            s = w0.kv_cache_mgr.allocate_sequence()
+            w0.prefill(torch.tensor([[1, 2, 3]], device="cuda"), s)
+            w0.decode_batch_tensor([4], [s])
+            del w0, s  # its graphs are garbage now
+            w1 = _wrapper(model, True)
+            s = w1.kv_cache_mgr.allocate_sequence()
+            w1.prefill(torch.tensor([[5, 6, 7, 8]], device="cuda"), s)
+            for t in range(3):
+                w1.decode_batch_tensor([9 + t], [s])
+    finally:
+        graph_decode.DecodeGraphs._forward = orig
+    assert any(c for c, _ in seen) and any(not c for c, _ in seen)
+    assert all(not on for capturing, on in seen if capturing)
+    assert gc.isenabled()
