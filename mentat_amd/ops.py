@@ -240,8 +240,9 @@ def semantic_ema(vectors: list, hidden: torch.Tensor, fresh: list, alpha: float)
     for v in vectors:
         _require(v.dtype == hidden.dtype and v.device == dev and v.is_contiguous() and v.numel() == H,
                  "every vector must be a contiguous H-element tensor of hidden's dtype and device")
+    # pinned + asynchronous: the host does not wait for queued GPU work here
     meta = torch.tensor([v.data_ptr() for v in vectors] + [int(bool(f)) for f in fresh], dtype=torch.int64)
-    meta = meta.to(dev)
+    meta = meta.pin_memory().to(dev, non_blocking=True)
     init = meta[n:].to(torch.int32)
     st = get_lib().mentat_semantic_ema(ptr(meta), ptr(hidden), ptr(init), n, H, hidden.stride(0),
                                        float(np.float32(1.0 - alpha)), float(np.float32(alpha)),

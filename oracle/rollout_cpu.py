@@ -5,8 +5,9 @@ Restates, in torch on the host, one prompt's rollout as the reference runs it
 (prompts are serial there, mentat_rollout.py:256-259):
   * prefill (core/generator_utils.py:306-338): the prompt through the model
     with causal SDPA (oracle.attention.reference_cpu_prefill), K/V appended
-    into per-layer paged pools with the reference's block bookkeeping
-    (oracle.paged_cache.OracleCache, copy-on-write copies applied to the pools);
+    into paged pools with the reference's block bookkeeping
+    (oracle.paged_cache.OracleCache, copy-on-write copies applied to the pools;
+    one store indexed by block id serves every layer);
   * decode steps (core/generator_utils.py:340-418, core/generator.py:174-207):
     every active leaf in DFS order through one batched forward; per layer the
     Q/K/V projections, RoPE at the kv length read before the layer loop, the
@@ -22,10 +23,11 @@ Restates, in torch on the host, one prompt's rollout as the reference runs it
 Metric as the reference's (core/generator.py:190, :508-511): live leaves
 summed over decode steps / decode wall time.
 
-The gate/branch/extend/prune rules are the ones pinned elsewhere (the cfg-1
-golden trajectory pins the product generator; the formulas here are the same
-restatements used by oracle.sampling). This file is a throughput baseline:
-its token choices are not compared with anything.
+Pinned by tests/test_gpu_batch_generator.py::
+test_cpu_rollout_restatement_follows_the_generator: on the fp32 plumbing model
+with the absolute gate it produces the product generator's live-leaf trace
+(the product generator is in turn pinned by the reference's own cfg-1
+trajectory). It is used as a throughput baseline.
 """
 from __future__ import annotations
 
@@ -66,8 +68,13 @@ class _CpuModel:
         self.B = block_size
         dt = next(model.parameters()).dtype
         self.cache = OracleCache(self.L, max_blocks, block_size)
-        self.kp = [torch.zeros(max_blocks, block_size, self.Hkv, self.D, dtype=dt) for _ in range(self.L)]
-        self.vp = [torch.zeros(max_blocks, block_size, self.Hkv, self.D, dtype=dt) for _ in range(self.L)]
+        # One K and one V store indexed by block id for every layer: the single
+        # allocator gives each id to one layer at a time, so per-layer pools
+        # (core/paged_kv_cache.py:124-138) would hold the same data.
+        ks = torch.zeros(max_blocks, block_size, self.Hkv, self.D, dtype=dt)
+        vs = torch.zeros(max_blocks, block_size, self.Hkv, self.D, dtype=dt)
+        self.kp = [ks] * self.L
+        self.vp = [vs] * self.L
 
     def _apply_copies(self, n0: int) -> None:
         for layer, src, dst in self.cache.copies[n0:]:
@@ -129,7 +136,7 @@ def reference_cpu_rollout(model, prompt_ids: list[int], *, max_new_tokens: int, 
                           max_active_branches: int = 8, branching_factor: int = 3, entropy_threshold: float = 2.5,
                           temperature: float = 0.7, repetition_penalty: float = 1.2, ema_alpha: float = 0.3,
                           semantic_similarity_threshold: float = 0.85, min_steps_before_prune: int = 5,
-                          eos_token_id: int = 2, block_size: int = 16, max_blocks: int = 1024) -> dict:
+                          eos_token_id: int = 2, block_size: int = 16, max_blocks: int = 8192) -> dict:
     """One prompt's rollout on the CPU until max_new_tokens or until decode time
     exceeds time_budget_s. Returns decode tokens, decode seconds, steps and the
     live-leaf trace."""
