@@ -165,6 +165,8 @@ struct RowShared {
   int32_t bi[kRowWaves];
   uint32_t chunk_tot[64];
   uint32_t cc[64 * 16];  // per-chunk counts of the last radix level's values (<= 16 of them)
+  uint32_t cc2[64 * 16]; // the same for a second level-0 bin (single-pass sampler)
+  uint64_t hn[16];       // level 1 of the nucleus-boundary bin (single-pass sampler)
   int32_t scan[kRowThreads];
 };
 
@@ -563,27 +565,118 @@ __global__ __launch_bounds__(kRowThreads) void row_stats_kernel(RowParams p) {
   // Mass of one token with key kk (every such token has the value key_to_float(kk)).
   auto key_mass = [&](uint32_t kk) -> uint64_t { return det_q((key_to_float(kk) - m_pen) * p.samp_c); };
 
-  uint32_t key_n;
-  uint64_t above_n;
-  select(need - 1, false, key_n, above_n);
-  const uint64_t qn = key_mass(key_n);
-  const uint64_t jn = (need - 1 - above_n) / qn;  // 0-based index of the last kept tie
-  const uint64_t kept_mass = above_n + (jn + 1) * qn;
-
   uint32_t c4[4] = {(uint32_t)row, (uint32_t)p.step, (uint32_t)(p.step >> 32), 0u};
   philox4x32_10(c4, (uint32_t)p.seed, (uint32_t)(p.seed >> 32));
   const uint64_t U = ((uint64_t)c4[0] << 32) | c4[1];
-  const uint64_t r = (uint64_t)(((unsigned __int128)U * kept_mass) >> 64);
+  auto mulhi = [](uint64_t a, uint64_t b) -> uint64_t { return (uint64_t)(((unsigned __int128)a * b) >> 64); };
 
-  uint32_t key_r;
-  uint64_t above_r;
-  select(r, kChunkCounts, key_r, above_r);
+  uint32_t key_r = 0;
+  uint64_t above_r = 0, r = 0;
+  bool fast = false, have_cc = false;
+  if constexpr (NLEV == 2 && kChunkCounts) {
+    // Both selections in one data pass. The nucleus boundary lies in level-0 bin
+    // bn, so the kept mass is in (above_bn, above_bn + mass(bn)] and the draw
+    // position r = U*kept/2^64 in [U*above_bn, U*(above_bn + mass(bn))] / 2^64:
+    // only the level-0 bins blo..bhi meeting that interval (a contiguous range of
+    // bins, keys descending) can hold the draw. One pass builds the level-1
+    // histogram of bn and of every bin of the range (per-chunk counts too when
+    // the range has at most two bins); a range wider than kRange bins takes the
+    // two-pass path below.
+    constexpr int kRange = (int)(sizeof(sh.hist1) / (16 * sizeof(uint64_t)));  // 256 bins
+    uint64_t* ch = sh.hist1;  // [kRange][16] level 1 of the range's bins, index bhi - b
+    uint64_t above_bn;
+    const uint32_t bn = pick_bin(sh.hist0, L0, run0, need - 1, above_bn);
+    const uint64_t mass_bn = sh.hist0[bn];
+    const uint64_t r_lo = mulhi(U, above_bn), r_hi = mulhi(U, above_bn + mass_bn);
+    uint64_t a_hi, a_lo;
+    const int bhi = (int)pick_bin(sh.hist0, L0, run0, r_lo, a_hi);  // the range's first bin (largest keys)
+    const int blo = (int)pick_bin(sh.hist0, L0, run0, r_hi, a_lo);
+    const int len = bhi - blo + 1;
+    if (len <= kRange) {
+      have_cc = len <= 2;
+      for (int t = tid; t < len * 16; t += kRowThreads) ch[t] = 0;
+      if (tid < 16) sh.hn[tid] = 0;
+      if (have_cc)
+        for (int t = tid; t < kMaxChunks * 16; t += kRowThreads) { sh.cc[t] = 0; sh.cc2[t] = 0; }
+      __syncthreads();
+      constexpr int shift1 = 32 - L0 - 4;
+      ROW_FOR_GROUPS(
+        const int i0 = (c * kRowThreads + tid) * EPV;
+        static_for<EPV>([&](auto ec_) __attribute__((always_inline)) {
+          constexpr int e = decltype(ec_)::value;
+          if (i0 + e >= p.V) return;
+          const float xp = penal(i0 + e, x[e]);
+          const uint32_t k = RE::key(xp);
+          const int b0 = (int)(k >> (32 - L0));
+          const bool in_n = b0 == (int)bn, in_r = b0 >= blo && b0 <= bhi;
+          if (!in_n && !in_r) return;
+          const uint32_t sub = (k >> shift1) & 15u;
+          const float ys = (xp - m_pen) * p.samp_c;
+          const uint64_t q = ys >= -41.0f ? det_q(ys) : 0;
+          if (in_n && q) atomicAdd((unsigned long long*)&sh.hn[sub], (unsigned long long)q);
+          if (in_r) {
+            const int ri = bhi - b0;
+            if (q) atomicAdd((unsigned long long*)&ch[ri * 16 + sub], (unsigned long long)q);
+            if (have_cc) atomicAdd(ri == 0 ? &sh.cc[c * 16 + sub] : &sh.cc2[c * 16 + sub], 1u);
+          }
+            });
+      )
+      __syncthreads();
+      // The boundary key (level 1 of bn, keys descending), its tie index, the kept mass, r.
+      uint64_t run = above_bn, above_n = above_bn;
+      uint32_t sub_n = 0;
+      for (int sb = 15; sb >= 0; --sb) {
+        const uint64_t h = sh.hn[sb];
+        if (h != 0 && run <= need - 1 && need - 1 < run + h) { sub_n = (uint32_t)sb; above_n = run; break; }
+        run += h;
+      }
+      const uint32_t key_n = ((bn << 4) | sub_n) << shift1;
+      const uint64_t qn = key_mass(key_n);
+      const uint64_t jn = (need - 1 - above_n) / qn;
+      r = mulhi(U, above_n + (jn + 1) * qn);
+      // The range bin holding r: thread t takes bin bhi - t, the masses above by a scan.
+      const uint64_t hb = tid < len ? sh.hist0[bhi - tid] : 0;
+      uint64_t tot_unused;
+      const uint64_t ab = a_hi + block_excl_scan_u64(hb, tot_unused, sh);
+      if (tid == 0) sh.sel[2] = 0xffffffffu;
+      __syncthreads();
+      if (tid < len && hb != 0 && ab <= r && r < ab + hb) { sh.sel[2] = (uint32_t)tid; sh.sel64[2] = ab; }
+      __syncthreads();
+      const uint32_t ri = sh.sel[2];
+      if (ri != 0xffffffffu) {
+        run = sh.sel64[2];
+        uint32_t sub_r = 0;
+        above_r = run;
+        for (int sb = 15; sb >= 0; --sb) {
+          const uint64_t h = ch[ri * 16 + sb];
+          if (h != 0 && run <= r && r < run + h) { sub_r = (uint32_t)sb; above_r = run; break; }
+          run += h;
+        }
+        key_r = (((uint32_t)(bhi - (int)ri) << 4) | sub_r) << shift1;
+        if (have_cc && ri == 1)
+          for (int t = tid; t < kMaxChunks * 16; t += kRowThreads) sh.cc[t] = sh.cc2[t];
+        fast = true;
+      }
+      __syncthreads();
+    }
+  }
+  if (!fast) {
+    uint32_t key_n;
+    uint64_t above_n;
+    select(need - 1, false, key_n, above_n);
+    const uint64_t qn = key_mass(key_n);
+    const uint64_t jn = (need - 1 - above_n) / qn;  // 0-based index of the last kept tie
+    const uint64_t kept_mass = above_n + (jn + 1) * qn;
+    r = mulhi(U, kept_mass);
+    select(r, kChunkCounts, key_r, above_r);
+  }
   const uint64_t qr = key_mass(key_r);
   const uint32_t j = (uint32_t)((r - above_r) / qr);  // the j-th (0-based) token of key_r by index
 
   // The j-th token with key_r in index order: per-chunk totals, then a thread scan
   // over the chunk that holds it.
-  if constexpr (kChunkCounts) {
+  // (The single-pass sampler counted per chunk only for ranges of at most two bins.)
+  if (kChunkCounts && (!fast || have_cc)) {
     const uint32_t lastv = (key_r >> (32 - kKeyBitsUsed)) & ((1u << LAST_BITS) - 1);
     if (tid < kMaxChunks) sh.chunk_tot[tid] = tid < nchunks ? sh.cc[tid * 16 + lastv] : 0u;
   } else {
