@@ -101,47 +101,47 @@ _Pragma("clang loop unroll(full)")
 template <typename T> struct RowElem;
 template <> struct RowElem<BF16> {
   static constexpr int EPV = 8;
-  __device__ static float get(const uint4& w, int e) {
+  __device__ __forceinline__ static float get(const uint4& w, int e) {
     const uint32_t d = e < 2 ? w.x : e < 4 ? w.y : e < 6 ? w.z : w.w;
     return (e & 1) ? bf16_hi(d) : bf16_lo(d);
   }
-  __device__ static float round(float v) { return __uint_as_float(((uint32_t)f32_to_bf16(v)) << 16); }
+  __device__ __forceinline__ static float round(float v) { return __uint_as_float(((uint32_t)f32_to_bf16(v)) << 16); }
   // Order-preserving 32-bit key of a value of this dtype (only the top 16 bits vary).
-  __device__ static uint32_t key(float v) {
+  __device__ __forceinline__ static uint32_t key(float v) {
     const uint32_t u = __float_as_uint(v == 0.f ? 0.f : v);  // -0 and +0 tie, as in float order
     return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
   }
-  __device__ static float scalar(const void* p, long i) { return Elem<BF16>::load1(p, i); }
+  __device__ __forceinline__ static float scalar(const void* p, long i) { return Elem<BF16>::load1(p, i); }
   // Radix levels (bits, most significant first) covering the key bits that vary.
   static constexpr int nlevels = 2;
   static constexpr int level_bits[3] = {12, 4, 0};
 };
 template <> struct RowElem<F16> {
   static constexpr int EPV = 8;
-  __device__ static float get(const uint4& w, int e) {
+  __device__ __forceinline__ static float get(const uint4& w, int e) {
     const uint32_t d = e < 2 ? w.x : e < 4 ? w.y : e < 6 ? w.z : w.w;
     return f16_bits_to_f32((uint16_t)((e & 1) ? (d >> 16) : (d & 0xffffu)));
   }
-  __device__ static float round(float v) { return f16_bits_to_f32(f32_to_f16_bits(v)); }
-  __device__ static uint32_t key(float v) {
+  __device__ __forceinline__ static float round(float v) { return f16_bits_to_f32(f32_to_f16_bits(v)); }
+  __device__ __forceinline__ static uint32_t key(float v) {
     const uint32_t u = __float_as_uint(v == 0.f ? 0.f : v);  // -0 and +0 tie, as in float order
     return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
   }
-  __device__ static float scalar(const void* p, long i) { return Elem<F16>::load1(p, i); }
+  __device__ __forceinline__ static float scalar(const void* p, long i) { return Elem<F16>::load1(p, i); }
   static constexpr int nlevels = 3;
   static constexpr int level_bits[3] = {12, 12, 8};
 };
 template <> struct RowElem<F32> {
   static constexpr int EPV = 4;
-  __device__ static float get(const uint4& w, int e) {
+  __device__ __forceinline__ static float get(const uint4& w, int e) {
     return __uint_as_float(e == 0 ? w.x : e == 1 ? w.y : e == 2 ? w.z : w.w);
   }
-  __device__ static float round(float v) { return v; }
-  __device__ static uint32_t key(float v) {
+  __device__ __forceinline__ static float round(float v) { return v; }
+  __device__ __forceinline__ static uint32_t key(float v) {
     const uint32_t u = __float_as_uint(v == 0.f ? 0.f : v);  // -0 and +0 tie, as in float order
     return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
   }
-  __device__ static float scalar(const void* p, long i) { return ((const float*)p)[i]; }
+  __device__ __forceinline__ static float scalar(const void* p, long i) { return ((const float*)p)[i]; }
   static constexpr int nlevels = 3;
   static constexpr int level_bits[3] = {12, 12, 8};
 };
@@ -154,21 +154,24 @@ __device__ __forceinline__ float key_to_float(uint32_t k) {
 // ---- block reductions (1024 threads) ----------------------------------------------------------
 constexpr int kHistBins = 4096;  // widest radix level: 12 key bits
 
-struct RowShared {
-  float f[kRowWaves * 4];
-  uint64_t u[kRowWaves];
+template <int NW>
+struct RowSharedT {
+  static constexpr int kWaves = NW;
+  float f[NW * 4];
+  uint64_t u[NW];
   uint64_t hist0[kHistBins];  // first radix level (shared by both selections)
   uint64_t hist1[kHistBins];  // deeper levels
   uint32_t sel[4];
   uint64_t sel64[4];
-  float bk[kRowWaves];
-  int32_t bi[kRowWaves];
+  float bk[NW];
+  int32_t bi[NW];
   uint32_t chunk_tot[64];
   uint32_t cc[64 * 16];  // per-chunk counts of the last radix level's values (<= 16 of them)
   uint32_t cc2[64 * 16]; // the same for a second level-0 bin (single-pass sampler)
   uint64_t hn[16];       // level 1 of the nucleus-boundary bin (single-pass sampler)
-  int32_t scan[kRowThreads];
+  int32_t scan[NW * 64];
 };
+using RowShared = RowSharedT<kRowWaves>;
 
 __device__ __forceinline__ float wave_max(float v) {
 _Pragma("clang loop unroll(full)")
@@ -190,8 +193,8 @@ _Pragma("clang loop unroll(full)")
 }
 
 // Reduce up to 4 floats at once: op 0 = max, 1 = sum (per value).
-template <int NVAL>
-__device__ __forceinline__ void block_reduce(float (&v)[NVAL], const int (&op)[NVAL], RowShared& sh) {
+template <int NVAL, class SH>
+__device__ __forceinline__ void block_reduce(float (&v)[NVAL], const int (&op)[NVAL], SH& sh) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
 _Pragma("clang loop unroll(full)")
   for (int i = 0; i < NVAL; ++i) v[i] = op[i] == 0 ? wave_max(v[i]) : wave_sum(v[i]);
@@ -204,18 +207,19 @@ _Pragma("clang loop unroll(full)")
 _Pragma("clang loop unroll(full)")
   for (int i = 0; i < NVAL; ++i) {
     float a = op[i] == 0 ? kNegInf : 0.f;
-    for (int w = 0; w < kRowWaves; ++w) a = op[i] == 0 ? fmaxf(a, sh.f[w * 4 + i]) : a + sh.f[w * 4 + i];
+    for (int w = 0; w < SH::kWaves; ++w) a = op[i] == 0 ? fmaxf(a, sh.f[w * 4 + i]) : a + sh.f[w * 4 + i];
     v[i] = a;
   }
 }
-__device__ __forceinline__ uint64_t block_sum_u64(uint64_t v, RowShared& sh) {
+template <class SH>
+__device__ __forceinline__ uint64_t block_sum_u64(uint64_t v, SH& sh) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   v = wave_sum_u64(v);
   __syncthreads();
   if (lane == 0) sh.u[wave] = v;
   __syncthreads();
   uint64_t a = 0;
-  for (int w = 0; w < kRowWaves; ++w) a += sh.u[w];
+  for (int w = 0; w < SH::kWaves; ++w) a += sh.u[w];
   return a;
 }
 
@@ -225,7 +229,8 @@ __device__ __forceinline__ uint64_t shfl_up_u64(uint64_t v, int o) {
   const uint32_t lo = __shfl_up((uint32_t)v, o), hi = __shfl_up((uint32_t)(v >> 32), o);
   return ((uint64_t)hi << 32) | lo;
 }
-__device__ __forceinline__ uint64_t block_excl_scan_u64(uint64_t v, uint64_t& total, RowShared& sh) {
+template <class SH>
+__device__ __forceinline__ uint64_t block_excl_scan_u64(uint64_t v, uint64_t& total, SH& sh) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   uint64_t inc = v;
 _Pragma("clang loop unroll(full)")
@@ -237,7 +242,7 @@ _Pragma("clang loop unroll(full)")
   if (lane == 63) sh.u[wave] = inc;
   __syncthreads();
   uint64_t base = 0, tot = 0;
-  for (int w = 0; w < kRowWaves; ++w) {
+  for (int w = 0; w < SH::kWaves; ++w) {
     const uint64_t t = sh.u[w];
     base += w < wave ? t : 0;
     tot += t;
@@ -319,17 +324,18 @@ constexpr int kRowUnroll = 8;
 constexpr int kMaxChunks = 64;                              // chunks of 1024 x EPV elements
 constexpr int kMaxPenWords = kMaxChunks * kRowThreads * 8 / 32;  // penalty bits (V <= 524288)
 
-template <typename T, bool AL>
-__global__ __launch_bounds__(kRowThreads) void row_stats_kernel(RowParams p) {
+// The multi-pass row algorithm for any dtype, with NT threads per row: `sh` and `pbits`
+// (penalty bits, (V + 31) / 32 words) are LDS of the calling kernel.
+template <typename T, bool AL, int NT>
+__device__ __forceinline__ void rows_generic(const RowParams& p, const int row, RowSharedT<NT / 64>& sh,
+                                             uint32_t* pbits) {
+  constexpr int kRowThreads = NT;
+  constexpr int kRowWaves = NT / 64;
   using RE = RowElem<T>;
   using S = typename T::storage;
   constexpr int EPV = RE::EPV;
-  const int row = blockIdx.x;
-  if (row >= p.R) return;
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
-  __shared__ RowShared sh;
-  __shared__ uint32_t pbits[kMaxPenWords];
   const char* rp = (const char*)p.logits + (long)row * p.row_stride * (long)sizeof(S);
   const int nchunks = (p.V + kRowThreads * EPV - 1) / (kRowThreads * EPV);
   const __amdgpu_buffer_rsrc_t rs =
@@ -720,6 +726,585 @@ _Pragma("clang loop unroll(full)")
   }
 }
 
+// ---- 16-bit logits: histogram of every value ------------------------------------------------
+// Every token's 16-bit value is counted into a histogram of all 65,536 values (two 16-bit counts
+// per LDS word) in one read of the row. A token's sampler mass, entropy terms and log-prob depend
+// on its value alone, so the row max (largest value present), both entropies, the log-sum-exp,
+// the nucleus and the draw's value and tie index are all resolved from the counts; a second read
+// (mostly from the last-level cache) then finds the drawn token's index and the top-K.
+// Rows with a count past 65,535 (one value repeated that often) or a non-finite value take the
+// multi-pass path. Key order: sign-magnitude bits mapped to unsigned order; -0 is counted as +0,
+// which compares equal to it.
+template <typename T> struct Bits16;
+template <> struct Bits16<BF16> {
+  __device__ __forceinline__ static float val(uint32_t raw) { return __uint_as_float(raw << 16); }
+  __device__ __forceinline__ static uint32_t raw(float v) { return __float_as_uint(v) >> 16; }  // v a bf16 value
+  static constexpr uint32_t kPosInfRaw = 0x7f80u, kNegInfRaw = 0xff80u;
+};
+template <> struct Bits16<F16> {
+  __device__ __forceinline__ static float val(uint32_t raw) { return f16_bits_to_f32((uint16_t)raw); }
+  __device__ __forceinline__ static uint32_t raw(float v) { return f32_to_f16_bits(v); }  // v an f16 value
+  static constexpr uint32_t kPosInfRaw = 0x7c00u, kNegInfRaw = 0xfc00u;
+};
+__host__ __device__ constexpr uint32_t key16(uint32_t raw) { return raw ^ ((raw & 0x8000u) ? 0xffffu : 0x8000u); }
+__device__ __forceinline__ uint32_t raw16_of_key(uint32_t k) { return k ^ ((k & 0x8000u) ? 0x8000u : 0xffffu); }
+
+constexpr int kFT = 1024;                                      // threads per row
+constexpr int kFW = kFT / 64;
+constexpr int kFastChunks = 20;                                // chunks of kFT 16-byte groups
+constexpr int kFastMaxV = kFastChunks * kFT * 8;               // 163,840 (the penalty bits' LDS)
+constexpr int kFastPenWords = kFastMaxV / 32;
+constexpr int kHistWords = 32768;                              // 65,536 16-bit counts
+constexpr int kSlabBins = 256;                                 // four bins (two words) per lane
+constexpr int kSlabs = 65536 / kSlabBins;
+constexpr int kCandCap = kFT;                                  // top-K candidates kept in LDS
+
+struct FastShared {
+  static constexpr int kWaves = kFW;
+  uint64_t slab_mass[kSlabs];  // sampler mass per slab of 256 values
+  uint32_t slab_cnt[kSlabs];   // tokens per slab
+  float f[kFW * 4];
+  uint64_t u[kFW];
+  uint32_t g[kFW * 4];
+  uint32_t sel[4];
+  uint64_t sel64[4];
+  float bk[kFW];
+  int32_t bi[kFW];
+  uint32_t ncand;
+};
+
+__device__ __forceinline__ uint64_t shfl_down_u64(uint64_t v, int o) {
+  const uint32_t lo = __shfl_down((uint32_t)v, o), hi = __shfl_down((uint32_t)(v >> 32), o);
+  return ((uint64_t)hi << 32) | lo;
+}
+__device__ __forceinline__ uint32_t wave_sum_u32(uint32_t v) {
+_Pragma("clang loop unroll(full)")
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
+_Pragma("clang loop unroll(full)")
+  for (int o = 32; o >= 1; o >>= 1) v = min(v, (uint32_t)__shfl_xor(v, o));
+  return v;
+}
+
+// Rows must start on 16-byte boundaries (16-byte buffer loads).
+template <typename T>
+__global__ __launch_bounds__(kFT) void row_stats_fast_kernel(RowParams p) {
+  constexpr bool AL = true;
+  using RE = RowElem<T>;
+  using B16 = Bits16<T>;
+  using S = typename T::storage;
+  constexpr int EPV = 8;
+  constexpr uint32_t kInfKey = key16(B16::kPosInfRaw), kNegInfKey = key16(B16::kNegInfRaw);
+  const int row = blockIdx.x;
+  if (row >= p.R) return;
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63;
+  __shared__ __align__(16) uint32_t hist[kHistWords];
+  __shared__ uint32_t pbits[kFastPenWords];
+  __shared__ FastShared fs;
+  static_assert(sizeof(RowSharedT<kFW>) <= sizeof(hist), "the multi-pass path reuses the histogram's LDS");
+  const int V = p.V;
+  const char* rp = (const char*)p.logits + (long)row * p.row_stride * (long)sizeof(S);
+  const int nchunks = (V + kFT * EPV - 1) / (kFT * EPV);
+  const __amdgpu_buffer_rsrc_t rs =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(rp), (short)0, V * (int)sizeof(S), 0x00020000);
+  // chunk c's group of this thread: the chunk offset rides in the scalar offset operand
+  auto load_raw = [&](int c) __attribute__((always_inline)) -> uint4 {
+    return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
+        rs, tid * EPV * (int)sizeof(S), c * kFT * EPV * (int)sizeof(S), 0));
+  };
+  auto pen_value = [&](float x) __attribute__((always_inline)) -> float {
+    return RE::round(x > 0.f ? __fdiv_rn(x, p.penalty) : x * p.penalty);
+  };
+  auto nkey = [](float v) __attribute__((always_inline)) -> uint32_t { return key16(B16::raw(v == 0.f ? 0.f : v)); };
+  auto kval = [](uint32_t k) __attribute__((always_inline)) -> float { return B16::val(raw16_of_key(k)); };
+
+  const bool use_pen = p.penalty != 1.0f && p.pen_offsets != nullptr;
+  const int nwords = (V + 31) / 32;
+  {
+    uint4* h4 = reinterpret_cast<uint4*>(hist);
+    for (int t = tid; t < kHistWords / 4; t += kFT) h4[t] = make_uint4(0u, 0u, 0u, 0u);
+  }
+  __syncthreads();
+
+  // ---- pass A: count the raw values (kRowUnroll 16-byte loads in flight per thread) ----
+  auto count1 = [&](uint32_t k) __attribute__((always_inline)) { atomicAdd(&hist[k >> 1], 1u << ((k & 1u) << 4)); };
+  for (int c0 = 0; c0 < nchunks; c0 += kRowUnroll) {
+    uint4 w[kRowUnroll];
+_Pragma("clang loop unroll(full)")
+    for (int u = 0; u < kRowUnroll; ++u) w[u] = load_raw(c0 + u);  // zeros past the row
+_Pragma("clang loop unroll(full)")
+    for (int u = 0; u < kRowUnroll; ++u) {
+      const int c = c0 + u;
+      if (c >= nchunks) break;
+      const int i0 = (c * kFT + tid) * EPV;
+      const uint32_t dw[4] = {w[u].x, w[u].y, w[u].z, w[u].w};
+      if (i0 + EPV <= V) {
+_Pragma("clang loop unroll(full)")
+        for (int k = 0; k < 4; ++k) {
+          // both halves' keys at once: xor 0xffff into a negative half, 0x8000 into a positive one
+          const uint32_t k2 = dw[k] ^ ((((dw[k] >> 15) & 0x10001u) * 0x7fffu) | 0x80008000u);
+          count1(k2 & 0xffffu);
+          count1(k2 >> 16);
+        }
+      } else {
+        for (int e = 0; e < EPV; ++e)
+          if (i0 + e < V) count1(key16((dw[e >> 1] >> ((e & 1) * 16)) & 0xffffu));
+      }
+    }
+  }
+  __syncthreads();
+  // -0 (key 0x7fff, high half of word 0x3fff) joins +0 (key 0x8000, low half of word 0x4000).
+  auto merge_neg_zero = [&]() __attribute__((always_inline)) {
+    if (tid == 0) {
+      const uint32_t n = hist[0x3fff] >> 16;
+      if (n) {
+        hist[0x3fff] -= n << 16;
+        hist[0x4000] += n;
+      }
+    }
+    __syncthreads();
+  };
+  merge_neg_zero();
+
+  // Largest key present; false when a count overflowed (the counts then do not sum to V) or a
+  // value is not finite.
+  auto survey = [&](uint32_t& top) __attribute__((always_inline)) -> bool {
+    uint32_t mx = 0, mn = 0xffffffffu, sm = 0;
+    constexpr int kPer = kHistWords / kFT / 4;  // 16-byte words per thread
+    const uint4* h4 = reinterpret_cast<const uint4*>(hist) + tid * kPer;
+_Pragma("clang loop unroll(full)")
+    for (int q = 0; q < kPer; ++q) {
+      const uint4 w4 = h4[q];
+      const uint32_t ws[4] = {w4.x, w4.y, w4.z, w4.w};
+_Pragma("clang loop unroll(full)")
+      for (int k = 0; k < 4; ++k) {
+        const uint32_t bin = (uint32_t)((tid * kPer + q) * 4 + k) * 2u;
+        const uint32_t lo = ws[k] & 0xffffu, hi = ws[k] >> 16;
+        sm += lo + hi;
+        if (lo) { mx = max(mx, bin + 1u); mn = min(mn, bin); }
+        if (hi) { mx = max(mx, bin + 2u); mn = min(mn, bin + 1u); }
+      }
+    }
+_Pragma("clang loop unroll(full)")
+    for (int o = 32; o >= 1; o >>= 1) {
+      mx = max(mx, (uint32_t)__shfl_xor(mx, o));
+      mn = min(mn, (uint32_t)__shfl_xor(mn, o));
+      sm += __shfl_xor(sm, o);
+    }
+    __syncthreads();
+    if (lane == 0) { fs.g[wave * 4] = mx; fs.g[wave * 4 + 1] = mn; fs.g[wave * 4 + 2] = sm; }
+    __syncthreads();
+    mx = 0; mn = 0xffffffffu; sm = 0;
+    for (int w = 0; w < kFW; ++w) {
+      mx = max(mx, fs.g[w * 4]);
+      mn = min(mn, fs.g[w * 4 + 1]);
+      sm += fs.g[w * 4 + 2];
+    }
+    top = mx - 1u;
+    return sm == (uint32_t)V && mx > 0u && top < kInfKey && mn > kNegInfKey;
+  };
+
+  uint32_t top;
+  bool ok = survey(top);
+  const float m_raw = kval(top);
+  float H_T = 0.f;
+  if (ok && use_pen) {
+    // Entropy of the raw values, then every penalised token (each distinct id once: the one
+    // that clears its bit) moves to its penalised value; the bits are set again for pass B.
+    float a2[2] = {0.f, 0.f};
+    for (int i = 0; i < kHistWords / kFT; ++i) {
+      const int w = tid + i * kFT;
+      const uint32_t wd = hist[w];
+      if (!wd) continue;
+_Pragma("clang loop unroll(full)")
+      for (int h = 0; h < 2; ++h) {
+        const uint32_t n = (wd >> (16 * h)) & 0xffffu;
+        if (!n) continue;
+        const float y = (kval((uint32_t)(2 * w + h)) - m_raw) * p.ent_c;
+        const float e = fast_exp2(y);
+        a2[0] += (float)n * e;
+        a2[1] += e > 0.f ? (float)n * (e * y) : 0.f;
+      }
+    }
+    { const int op[2] = {1, 1}; block_reduce<2>(a2, op, fs); }
+    H_T = (log2f(a2[0]) - a2[1] / a2[0]) * kLn2;
+    // (the id list is read only now: its loads would otherwise wait for the row's)
+    for (int w = tid; w < nwords; w += kFT) pbits[w] = 0u;
+    __syncthreads();
+    const int b = p.pen_offsets[row], e = p.pen_offsets[row + 1];
+    for (int j = b + tid; j < e; j += kFT) {
+      const int id = p.pen_ids[j];
+      if (id >= 0 && id < V) atomicOr(&pbits[id >> 5], 1u << (id & 31));
+    }
+    __syncthreads();
+    for (int j = b + tid; j < e; j += kFT) {
+      const int id = p.pen_ids[j];
+      if (id < 0 || id >= V) continue;
+      const uint32_t bit = 1u << (id & 31);
+      if (atomicAnd(&pbits[id >> 5], ~bit) & bit) {
+        const float x = RE::scalar(rp, id);
+        const uint32_t kx = nkey(x), kp = nkey(pen_value(x));
+        if (kx != kp) {
+          atomicSub(&hist[kx >> 1], 1u << ((kx & 1u) << 4));
+          atomicAdd(&hist[kp >> 1], 1u << ((kp & 1u) << 4));
+        }
+      }
+    }
+    __syncthreads();
+    for (int j = b + tid; j < e; j += kFT) {
+      const int id = p.pen_ids[j];
+      if (id >= 0 && id < V) atomicOr(&pbits[id >> 5], 1u << (id & 31));
+    }
+    __syncthreads();
+    ok = survey(top);
+  }
+  if (!ok) {
+    __syncthreads();
+    rows_generic<T, AL, kFT>(p, row, *reinterpret_cast<RowSharedT<kFW>*>(hist), pbits);
+    return;
+  }
+  const float m_pen = kval(top);
+
+  // ---- resolution: one sweep over the slabs (wave w takes slabs w, w + 16, ...; lane l the
+  // four values 4l .. 4l + 3 of the slab) for the entropy sums, each slab's mass and count ----
+  const bool need_pen_sums = p.topk > 0 || p.out_entropy_pen != nullptr || p.out_lse != nullptr;
+  const bool want_mass = p.do_sample != 0, want_cnt = p.topk > 0;
+  auto unit_mass = [&](uint32_t k) __attribute__((always_inline)) -> uint64_t {
+    const float ys = (kval(k) - m_pen) * p.samp_c;
+    return ys >= -41.0f ? det_q(ys) : 0;
+  };
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int i = 0; i < kSlabs / kFW; ++i) {
+    const int s = wave + i * kFW;
+    const uint2 wd = reinterpret_cast<const uint2*>(hist)[s * (kSlabBins / 4) + lane];
+    uint64_t mass = 0;
+    uint32_t cnt = 0;
+    if (__any((wd.x | wd.y) != 0u)) {
+      if ((wd.x | wd.y) != 0u) {
+_Pragma("clang loop unroll(full)")
+        for (int b = 0; b < 4; ++b) {
+          const uint32_t n = ((b < 2 ? wd.x : wd.y) >> ((b & 1) * 16)) & 0xffffu;
+          if (!n) continue;
+          const uint32_t k = (uint32_t)(s * kSlabBins + lane * 4 + b);
+          const float v = kval(k), fn = (float)n;
+          if (!use_pen) {
+            const float y = (v - m_raw) * p.ent_c;
+            const float e = fast_exp2(y);
+            acc[0] += fn * e;
+            acc[1] += e > 0.f ? fn * (e * y) : 0.f;
+          }
+          if (need_pen_sums) {
+            const float y1 = (v - m_pen) * kLog2e;
+            const float e1 = fast_exp2(y1);
+            acc[2] += fn * e1;
+            acc[3] += e1 > 0.f ? fn * (e1 * y1) : 0.f;
+          }
+          if (want_mass) {
+            const float ys = (v - m_pen) * p.samp_c;
+            if (ys >= -41.0f) mass += (uint64_t)n * det_q(ys);
+          }
+          cnt += n;
+        }
+      }
+      if (want_mass) mass = wave_sum_u64(mass);
+      if (want_cnt) cnt = wave_sum_u32(cnt);
+    }
+    if (lane == 0) {
+      fs.slab_mass[s] = mass;
+      fs.slab_cnt[s] = cnt;
+    }
+  }
+  { const int op[4] = {1, 1, 1, 1}; block_reduce<4>(acc, op, fs); }
+  if (!use_pen) H_T = (log2f(acc[0]) - acc[1] / acc[0]) * kLn2;
+  const float H_pen = (log2f(acc[2]) - acc[3] / acc[2]) * kLn2;
+  const float logsum = logf(acc[2]);
+  if (tid == 0) {
+    p.out_entropy[row] = H_T;
+    if (p.out_entropy_pen) p.out_entropy_pen[row] = H_pen;
+    if (p.out_lse) p.out_lse[row] = m_pen + logsum;
+    if (p.out_gate) p.out_gate[row] = H_T > p.gate_threshold ? 1 : 0;
+  }
+  if (!p.do_sample && p.topk == 0) return;
+
+  // Slab holding position pos (largest keys first): thread t holds slab kSlabs - 1 - t with
+  // `mine` and the exclusive prefix `ex`.
+  auto find_slab = [&](uint64_t mine, uint64_t ex, uint64_t pos, uint64_t& above) __attribute__((always_inline)) -> int {
+    if (mine && ex <= pos && pos < ex + mine) {
+      fs.sel[0] = (uint32_t)(kSlabs - 1 - tid);
+      fs.sel64[0] = ex;
+    }
+    __syncthreads();
+    const int s = min((int)fs.sel[0], kSlabs - 1);  // pos is always inside the total
+    above = fs.sel64[0];
+    __syncthreads();
+    return s;
+  };
+  // Value holding position pos inside slab s (whose larger keys hold `above`), by sampler mass or
+  // by token count; wave 0 resolves it, every thread returns the key and the mass above it.
+  auto slab_pick = [&](int s, uint64_t above, uint64_t pos, bool by_mass, uint64_t& above_k) __attribute__((always_inline)) -> uint32_t {
+    if (wave == 0) {
+      const uint2 wd = reinterpret_cast<const uint2*>(hist)[s * (kSlabBins / 4) + lane];
+      uint64_t m[4], tot = 0;
+_Pragma("clang loop unroll(full)")
+      for (int b = 0; b < 4; ++b) {
+        const uint32_t n = ((b < 2 ? wd.x : wd.y) >> ((b & 1) * 16)) & 0xffffu;
+        const uint32_t k = (uint32_t)(s * kSlabBins + lane * 4 + b);
+        m[b] = n == 0 ? 0 : by_mass ? (uint64_t)n * unit_mass(k) : (uint64_t)n;
+        tot += m[b];
+      }
+      uint64_t inc = tot;  // suffix sum: lanes above hold larger keys
+_Pragma("clang loop unroll(full)")
+      for (int o = 1; o < 64; o <<= 1) {
+        const uint64_t t = shfl_down_u64(inc, o);
+        if (lane + o < 64) inc += t;
+      }
+      uint64_t run = above + (inc - tot);
+_Pragma("clang loop unroll(full)")
+      for (int b = 3; b >= 0; --b) {
+        if (m[b] && run <= pos && pos < run + m[b]) {
+          fs.sel[1] = (uint32_t)(s * kSlabBins + lane * 4 + b);
+          fs.sel64[1] = run;
+        }
+        run += m[b];
+      }
+    }
+    __syncthreads();
+    const uint32_t k = fs.sel[1] & 0xffffu;
+    above_k = fs.sel64[1];
+    __syncthreads();
+    return k;
+  };
+
+  // ---- the draw: nucleus boundary, kept mass, r, the drawn value and its tie index ----
+  float v_r = 0.f;
+  uint32_t j_r = 0;
+  if (p.do_sample) {
+    const uint64_t mine = tid < kSlabs ? fs.slab_mass[kSlabs - 1 - tid] : 0;
+    uint64_t Z;
+    const uint64_t ex = block_excl_scan_u64(mine, Z, fs);
+    uint64_t need = (uint64_t)(((unsigned __int128)Z * p.top_p_q32 + 0xffffffffull) >> 32);
+    if (need < 1) need = 1;
+    uint64_t a_s, above_n, above_r;
+    int s = find_slab(mine, ex, need - 1, a_s);
+    const uint32_t key_n = slab_pick(s, a_s, need - 1, true, above_n);
+    const uint64_t qn = unit_mass(key_n);
+    const uint64_t jn = (need - 1 - above_n) / qn;  // 0-based index of the last kept tie
+    const uint64_t kept = above_n + (jn + 1) * qn;
+    uint32_t c4[4] = {(uint32_t)row, (uint32_t)p.step, (uint32_t)(p.step >> 32), 0u};
+    philox4x32_10(c4, (uint32_t)p.seed, (uint32_t)(p.seed >> 32));
+    const uint64_t U = ((uint64_t)c4[0] << 32) | c4[1];
+    const uint64_t r = (uint64_t)(((unsigned __int128)U * kept) >> 64);
+    s = find_slab(mine, ex, r, a_s);
+    const uint32_t key_r = slab_pick(s, a_s, r, true, above_r);
+    j_r = (uint32_t)((r - above_r) / unit_mass(key_r));
+    v_r = kval(key_r);
+  }
+  // ---- top-K: candidates are the values whose log-prob is at least the K-th token's ----
+  float v_thr = __builtin_huge_valf();
+  if (p.topk > 0) {
+    const uint64_t mine = tid < kSlabs ? fs.slab_cnt[kSlabs - 1 - tid] : 0;
+    uint64_t tot, a_s, a_k;
+    const uint64_t ex = block_excl_scan_u64(mine, tot, fs);
+    const int s = find_slab(mine, ex, (uint64_t)(p.topk - 1), a_s);
+    const uint32_t kb = slab_pick(s, a_s, (uint64_t)(p.topk - 1), false, a_k);
+    const float lpK = RE::round((kval(kb) - m_pen) - logsum);
+    if (wave == 0) {
+      // log-probs fall with the value: walk down from kb while they still equal lpK
+      uint32_t lowest = kb;
+      for (int s2 = (int)(kb / kSlabBins); s2 >= 0; --s2) {
+        const uint2 wd = reinterpret_cast<const uint2*>(hist)[s2 * (kSlabBins / 4) + lane];
+        bool stop = false;
+_Pragma("clang loop unroll(full)")
+        for (int b = 0; b < 4; ++b) {
+          const uint32_t n = ((b < 2 ? wd.x : wd.y) >> ((b & 1) * 16)) & 0xffffu;
+          const uint32_t k = (uint32_t)(s2 * kSlabBins + lane * 4 + b);
+          if (n && k < kb) {
+            if (RE::round((kval(k) - m_pen) - logsum) == lpK) lowest = min(lowest, k);
+            else stop = true;
+          }
+        }
+        lowest = wave_min_u32(lowest);
+        if (__any(stop)) break;
+      }
+      if (lane == 0) fs.sel[2] = lowest;
+    }
+    __syncthreads();
+    v_thr = kval(fs.sel[2]);
+  }
+
+  // ---- pass B (the row again): matches of the drawn value per (chunk, wave); top-K candidates ----
+  uint32_t* cnt = hist;                                      // [kFastChunks][kFW]
+  uint2* cand = reinterpret_cast<uint2*>(hist + 1024);       // [kCandCap] (log-prob bits, index)
+  const float v_match = p.do_sample ? v_r : __builtin_nanf("");  // NaN matches nothing
+  __syncthreads();
+  if (tid == 0) fs.ncand = 0;
+  __syncthreads();
+  for (int c0 = 0; c0 < nchunks; c0 += kRowUnroll) {
+    uint4 w[kRowUnroll];
+_Pragma("clang loop unroll(full)")
+    for (int u = 0; u < kRowUnroll; ++u) w[u] = load_raw(c0 + u);
+_Pragma("clang loop unroll(full)")
+    for (int u = 0; u < kRowUnroll; ++u) {
+      const int c = c0 + u;
+      if (c >= nchunks) break;
+      const int i0 = (c * kFT + tid) * EPV;
+      const uint4 d = w[u];
+      const uint32_t vm = i0 + EPV <= V ? 0xffu : i0 >= V ? 0u : (1u << (V - i0)) - 1u;  // valid elements
+      const uint32_t pb = (use_pen && i0 < V) ? (pbits[i0 >> 5] >> (i0 & 31)) & vm & 0xffu : 0u;
+      const uint32_t plain = vm & ~pb;
+      uint32_t m = 0, cm = 0;
+_Pragma("clang loop unroll(full)")
+      for (int e = 0; e < EPV; ++e) {
+        const float xv = RE::get(d, e);
+        const bool pl = ((plain >> e) & 1u) != 0;
+        m += (pl && xv == v_match) ? 1u : 0u;
+        cm |= (pl && xv >= v_thr) ? 1u << e : 0u;
+      }
+      if (p.do_sample) {
+        m = wave_sum_u32(m);
+        if (lane == 0) cnt[c * kFW + wave] = m;
+      }
+      // penalised elements and top-K candidates (both rare), one at a time
+      for (uint32_t bits = pb | cm; bits != 0u; bits &= bits - 1u) {
+        const int e = __builtin_ctz(bits);
+        float xv = RE::get(d, e);
+        if ((pb >> e) & 1u) {
+          xv = pen_value(xv);
+          if (xv == v_match) atomicAdd(&cnt[c * kFW + wave], 1u);
+          if (!(xv >= v_thr)) continue;
+        }
+        if (p.topk > 0) {
+          const uint32_t pos = atomicAdd(&fs.ncand, 1u);
+          if (pos < kCandCap)
+            cand[pos] = make_uint2(__float_as_uint(RE::round((xv - m_pen) - logsum)), (uint32_t)(i0 + e));
+        }
+      }
+    }
+  }
+  __syncthreads();
+
+  if (p.topk > 0) {
+    auto block_best = [&](float& bk, int& bi) __attribute__((always_inline)) {
+      for (int o = 32; o >= 1; o >>= 1) {
+        const float ok = __shfl_xor(bk, o);
+        const int oi = __shfl_xor(bi, o);
+        if (tk_better(ok, oi, bk, bi)) { bk = ok; bi = oi; }
+      }
+      __syncthreads();
+      if (lane == 0) { fs.bk[wave] = bk; fs.bi[wave] = bi; }
+      __syncthreads();
+      bk = fs.bk[0];
+      bi = fs.bi[0];
+      for (int w = 1; w < kFW; ++w)
+        if (tk_better(fs.bk[w], fs.bi[w], bk, bi)) { bk = fs.bk[w]; bi = fs.bi[w]; }
+    };
+    const uint32_t nc = fs.ncand;
+    if (nc <= (uint32_t)kCandCap) {
+      float ck = kNegInf;
+      int ci = 0x7fffffff;
+      if ((uint32_t)tid < nc) {
+        const uint2 e = cand[tid];
+        ck = __uint_as_float(e.x);
+        ci = (int)e.y;
+      }
+      for (int j = 0; j < p.topk; ++j) {
+        float bk = ck;
+        int bi = ci;
+        block_best(bk, bi);
+        if (tid == 0) {
+          if (p.out_topk) p.out_topk[(long)row * p.topk + j] = bi;
+          if (p.out_topk_lp) p.out_topk_lp[(long)row * p.topk + j] = bk;
+        }
+        if (ci == bi) { ck = kNegInf; ci = 0x7fffffff; }
+      }
+    } else {
+      // more tied candidates than LDS holds: K selections over the row, read again
+      float prev_k = __builtin_huge_valf();
+      int prev_i = -1;
+      for (int j = 0; j < p.topk; ++j) {
+        float bk = kNegInf;
+        int bi = 0x7fffffff;
+        for (int c = 0; c < nchunks; ++c) {
+          const int i0 = (c * kFT + tid) * EPV;
+          const uint4 w = load_raw(c);
+          const uint32_t pb = (use_pen && i0 < V) ? (pbits[i0 >> 5] >> (i0 & 31)) & 0xffu : 0u;
+          static_for<EPV>([&](auto ec_) __attribute__((always_inline)) {
+            constexpr int e = decltype(ec_)::value;
+            float xv = RE::get(w, e);
+            if ((pb >> e) & 1u) xv = pen_value(xv);
+            if (i0 + e < V && xv >= v_thr) {
+              const int i = i0 + e;
+              const float key = RE::round((xv - m_pen) - logsum);
+              const bool after = key < prev_k || (key == prev_k && i > prev_i);
+              if (after && tk_better(key, i, bk, bi)) { bk = key; bi = i; }
+            }
+          });
+        }
+        block_best(bk, bi);
+        if (tid == 0) {
+          if (p.out_topk) p.out_topk[(long)row * p.topk + j] = bi;
+          if (p.out_topk_lp) p.out_topk_lp[(long)row * p.topk + j] = bk;
+        }
+        prev_k = bk;
+        prev_i = bi;
+      }
+    }
+  }
+
+  // ---- the drawn token: the j_r-th (by index) token of value v_r ----
+  if (p.do_sample) {
+    const uint32_t v = tid < nchunks * kFW ? cnt[tid] : 0u;
+    if (tid == 0) fs.sel[3] = 0xffffffffu;
+    uint64_t tot;
+    const uint64_t ex = block_excl_scan_u64((uint64_t)v, tot, fs);
+    if (v && ex <= j_r && j_r < ex + v) {
+      fs.sel[3] = (uint32_t)tid;
+      fs.sel64[3] = ex;
+    }
+    __syncthreads();
+    const uint32_t t = fs.sel[3];
+    if (t != 0xffffffffu && wave == (int)(t % kFW)) {
+      const int cs = (int)(t / kFW);
+      const uint4 d = load_raw(cs);
+      const int i0 = (cs * kFT + tid) * EPV;
+      const uint32_t pb = (use_pen && i0 < V) ? (pbits[i0 >> 5] >> (i0 & 31)) & 0xffu : 0u;
+      uint32_t mt = 0;  // bit e: element e matches
+      for (int e = 0; e < EPV; ++e) {
+        float xv = RE::get(d, e);
+        if ((pb >> e) & 1u) xv = pen_value(xv);
+        if (i0 + e < V && xv == v_r) mt |= 1u << e;
+      }
+      const uint32_t m = (uint32_t)__builtin_popcount(mt);
+      uint32_t inc = m;
+      for (int o = 1; o < 64; o <<= 1) {
+        const uint32_t u = __shfl_up(inc, o);
+        if (lane >= o) inc += u;
+      }
+      uint32_t seen = (uint32_t)fs.sel64[3] + inc - m;
+      if (m && seen <= j_r && j_r < seen + m) {
+        for (int e = 0; e < EPV; ++e) {
+          if ((mt >> e) & 1u) {
+            if (seen == j_r && p.out_sample) p.out_sample[row] = i0 + e;
+            ++seen;
+          }
+        }
+      }
+    }
+  }
+}
+
+template <typename T, bool AL>
+__global__ __launch_bounds__(kRowThreads) void row_stats_kernel(RowParams p) {
+  const int row = blockIdx.x;
+  if (row >= p.R) return;
+  __shared__ RowShared sh;
+  __shared__ uint32_t pbits[kMaxPenWords];
+  rows_generic<T, AL, kRowThreads>(p, row, sh, pbits);
+}
+
 template <typename T>
 static int dispatch_rows(const RowParams& p, hipStream_t s) {
   constexpr int EPV = RowElem<T>::EPV;
@@ -728,6 +1313,12 @@ static int dispatch_rows(const RowParams& p, hipStream_t s) {
   if (nchunks > kMaxChunks || (long)p.V > (long)kMaxPenWords * 32) return MENTAT_EUNSUP;
   // 16-byte loads need every row to start on a 16-byte boundary.
   const bool aligned = (((uintptr_t)p.logits) & 15u) == 0 && ((p.row_stride * (long)sizeof(S)) & 15) == 0;
+  if constexpr (sizeof(S) == 2) {
+    if (aligned && p.V <= kFastMaxV) {
+      hipLaunchKernelGGL((row_stats_fast_kernel<T>), dim3(p.R), dim3(kFT), 0, s, p);
+      return (int)hipGetLastError();
+    }
+  }
   if (aligned)
     hipLaunchKernelGGL((row_stats_kernel<T, true>), dim3(p.R), dim3(kRowThreads), 0, s, p);
   else

@@ -120,3 +120,69 @@ def test_entropy_gate_sampling_step_full_size(gpu):
         assert abs(st.entropy[r].item() - H) < 1e-4 * H
         want, _, _, _ = S.top_p_sample(xs[r], 0.7, 0.9, seed=0, step=0, row=r)
         assert st.sample[r].item() == want, r
+
+
+def _edge_rows(kind, rng):
+    """float32 rows (before rounding to bf16) that steer the kernel onto one of its paths."""
+    if kind == "count_overflow":      # 70,000 tokens of one value: past a 16-bit count
+        V = 151936
+        x = rng.normal(0, 1, (3, V)).astype(np.float32)
+        for r in range(3):
+            x[r, rng.choice(V, 70000, replace=False)] = 0.5
+    elif kind == "masked_vocab":      # -inf entries (a masked vocabulary): not finite
+        V = 151936
+        x = rng.normal(0, 2, (3, V)).astype(np.float32)
+        x[:, rng.random((V,)) < 0.3] = -np.inf
+    elif kind == "signed_zeros":      # +0 and -0 tie: the draw orders them by index
+        V = 5000
+        x = rng.normal(0, 0.05, (4, V)).astype(np.float32)
+        for r in range(4):
+            z = rng.choice(V, 4400, replace=False)
+            x[r, z[:2200]] = 0.0
+            x[r, z[2200:]] = -0.0
+    elif kind in ("top_ties_in_lds", "top_ties_past_lds"):  # many tokens share the largest value
+        V = 32000
+        n = 300 if kind == "top_ties_in_lds" else 2000
+        x = np.clip(rng.normal(0, 1, (3, V)), -4, 2).astype(np.float32)
+        for r in range(3):
+            x[r, rng.choice(V, n, replace=False)] = 3.0
+    else:
+        raise ValueError(kind)
+    return x
+
+
+@pytest.mark.parametrize("kind", ["count_overflow", "masked_vocab", "signed_zeros", "top_ties_in_lds",
+                                  "top_ties_past_lds"])
+def test_edge_rows_match_oracle(gpu, kind):
+    """Rows that leave the one-read path (a count past 16 bits, -inf entries), signed zeros in the
+    nucleus, and top-K ties held in LDS or past its capacity: entropies, top-K and draws as the oracle."""
+    print(f"case row_stats edge rows {kind}", flush=True)
+    rng = np.random.default_rng(["count_overflow", "masked_vocab", "signed_zeros", "top_ties_in_lds",
+                                 "top_ties_past_lds"].index(kind) + 40)
+    x = torch.from_numpy(_edge_rows(kind, rng)).to(torch.bfloat16).to(gpu)
+    R, V = x.shape
+    lists, off, ids = _pen_csr(rng, R, V, 20, gpu)
+    K, T, top_p = 8, 0.8, 0.95
+    xs = x.float().cpu().numpy()
+    for step in (0, 7):
+        st = ops.row_stats(x, temperature=T, penalty=1.3, pen_offsets=off, pen_ids=ids, gate_threshold=3.0,
+                           topk=K, sample=True, sample_temperature=T, top_p=top_p, seed=99, step=step)
+        torch.cuda.synchronize()
+        for r in range(R):
+            H = S.entropy(xs[r], T)
+            assert abs(st.entropy[r].item() - H) < 1e-4 * max(1.0, H), (kind, r, st.entropy[r].item(), H)
+            xp = S.penalize(xs[r], lists[r], 1.3, "bf16")
+            want, _, _, _ = S.top_p_sample(xp, T, top_p, seed=99, step=step, row=r)
+            assert st.sample[r].item() == want, (kind, step, r)
+            keys = S.log_softmax_keys(xp, "bf16")
+            oid, oval = S.topk(keys, K)
+            gid = st.topk_ids[r].cpu().numpy()
+            glp = st.topk_lp[r].cpu().numpy()
+            ulp = 2.0 ** -5
+            np.testing.assert_allclose(glp, oval, rtol=0, atol=ulp * max(1.0, abs(float(oval[0]))))
+            for j in range(K):
+                near = np.abs(keys - oval[j]) <= ulp * max(1.0, abs(float(oval[j])))
+                if near.sum() == 1 or kind.startswith("top_ties"):
+                    assert gid[j] == oid[j], (kind, r, j, gid, oid)
+                else:
+                    assert near[gid[j]]
