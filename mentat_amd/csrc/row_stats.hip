@@ -766,11 +766,14 @@ struct FastShared {
   float f[kFW * 4];
   uint64_t u[kFW];
   uint32_t g[kFW * 4];
-  uint32_t sel[4];
-  uint64_t sel64[4];
+  uint32_t sel[8];     // one slot per resolution step
+  uint64_t sel64[8];
   float bk[kFW];
   int32_t bi[kFW];
   uint32_t ncand;
+  uint32_t total;      // tokens counted by the sweep
+  uint32_t top_pen;    // largest key a penalised token moved to
+  uint32_t bad;        // a penalised value is not finite
 };
 
 __device__ __forceinline__ uint64_t shfl_down_u64(uint64_t v, int o) {
@@ -827,10 +830,24 @@ __global__ __launch_bounds__(kFT) void row_stats_fast_kernel(RowParams p) {
     uint4* h4 = reinterpret_cast<uint4*>(hist);
     for (int t = tid; t < kHistWords / 4; t += kFT) h4[t] = make_uint4(0u, 0u, 0u, 0u);
   }
+  if (tid == 0) {
+    fs.total = 0;
+    fs.top_pen = 0;
+    fs.bad = 0;
+  }
   __syncthreads();
+  // The draw's uniform depends only on (seed, row, step).
+  uint64_t U = 0;
+  if (p.do_sample) {
+    uint32_t c4[4] = {(uint32_t)row, (uint32_t)p.step, (uint32_t)(p.step >> 32), 0u};
+    philox4x32_10(c4, (uint32_t)p.seed, (uint32_t)(p.seed >> 32));
+    U = ((uint64_t)c4[0] << 32) | c4[1];
+  }
 
-  // ---- pass A: count the raw values (kRowUnroll 16-byte loads in flight per thread) ----
+  // ---- pass A: count the raw values (kRowUnroll 16-byte loads in flight per thread); the
+  // largest and smallest keys on the way ----
   auto count1 = [&](uint32_t k) __attribute__((always_inline)) { atomicAdd(&hist[k >> 1], 1u << ((k & 1u) << 4)); };
+  uint32_t kmx = 0, kmn = 0xffffffffu;
   for (int c0 = 0; c0 < nchunks; c0 += kRowUnroll) {
     uint4 w[kRowUnroll];
 _Pragma("clang loop unroll(full)")
@@ -838,78 +855,62 @@ _Pragma("clang loop unroll(full)")
 _Pragma("clang loop unroll(full)")
     for (int u = 0; u < kRowUnroll; ++u) {
       const int c = c0 + u;
-      if (c >= nchunks) break;
       const int i0 = (c * kFT + tid) * EPV;
       const uint32_t dw[4] = {w[u].x, w[u].y, w[u].z, w[u].w};
-      if (i0 + EPV <= V) {
+      if (c >= nchunks) {
+      } else if (i0 + EPV <= V) {
 _Pragma("clang loop unroll(full)")
         for (int k = 0; k < 4; ++k) {
           // both halves' keys at once: xor 0xffff into a negative half, 0x8000 into a positive one
           const uint32_t k2 = dw[k] ^ ((((dw[k] >> 15) & 0x10001u) * 0x7fffu) | 0x80008000u);
-          count1(k2 & 0xffffu);
-          count1(k2 >> 16);
+          const uint32_t lo = k2 & 0xffffu, hi = k2 >> 16;
+          count1(lo);
+          count1(hi);
+          kmx = max(kmx, max(lo, hi));
+          kmn = min(kmn, min(lo, hi));
         }
       } else {
-        for (int e = 0; e < EPV; ++e)
-          if (i0 + e < V) count1(key16((dw[e >> 1] >> ((e & 1) * 16)) & 0xffffu));
+_Pragma("clang loop unroll(full)")
+        for (int e = 0; e < EPV; ++e) {
+          if (i0 + e < V) {
+            const uint32_t k = key16((dw[e >> 1] >> ((e & 1) * 16)) & 0xffffu);
+            count1(k);
+            kmx = max(kmx, k);
+            kmn = min(kmn, k);
+          }
+        }
       }
     }
   }
+_Pragma("clang loop unroll(full)")
+  for (int o = 32; o >= 1; o >>= 1) {
+    kmx = max(kmx, (uint32_t)__shfl_xor(kmx, o));
+    kmn = min(kmn, (uint32_t)__shfl_xor(kmn, o));
+  }
+  if (lane == 0) {
+    fs.g[wave * 2] = kmx;
+    fs.g[wave * 2 + 1] = kmn;
+  }
   __syncthreads();
   // -0 (key 0x7fff, high half of word 0x3fff) joins +0 (key 0x8000, low half of word 0x4000).
-  auto merge_neg_zero = [&]() __attribute__((always_inline)) {
-    if (tid == 0) {
-      const uint32_t n = hist[0x3fff] >> 16;
-      if (n) {
-        hist[0x3fff] -= n << 16;
-        hist[0x4000] += n;
-      }
+  if (tid == 0) {
+    const uint32_t n = hist[0x3fff] >> 16;
+    if (n) {
+      hist[0x3fff] -= n << 16;
+      hist[0x4000] += n;
     }
-    __syncthreads();
-  };
-  merge_neg_zero();
-
-  // Largest key present; false when a count overflowed (the counts then do not sum to V) or a
-  // value is not finite.
-  auto survey = [&](uint32_t& top) __attribute__((always_inline)) -> bool {
-    uint32_t mx = 0, mn = 0xffffffffu, sm = 0;
-    constexpr int kPer = kHistWords / kFT / 4;  // 16-byte words per thread
-    const uint4* h4 = reinterpret_cast<const uint4*>(hist) + tid * kPer;
-_Pragma("clang loop unroll(full)")
-    for (int q = 0; q < kPer; ++q) {
-      const uint4 w4 = h4[q];
-      const uint32_t ws[4] = {w4.x, w4.y, w4.z, w4.w};
-_Pragma("clang loop unroll(full)")
-      for (int k = 0; k < 4; ++k) {
-        const uint32_t bin = (uint32_t)((tid * kPer + q) * 4 + k) * 2u;
-        const uint32_t lo = ws[k] & 0xffffu, hi = ws[k] >> 16;
-        sm += lo + hi;
-        if (lo) { mx = max(mx, bin + 1u); mn = min(mn, bin); }
-        if (hi) { mx = max(mx, bin + 2u); mn = min(mn, bin + 1u); }
-      }
-    }
-_Pragma("clang loop unroll(full)")
-    for (int o = 32; o >= 1; o >>= 1) {
-      mx = max(mx, (uint32_t)__shfl_xor(mx, o));
-      mn = min(mn, (uint32_t)__shfl_xor(mn, o));
-      sm += __shfl_xor(sm, o);
-    }
-    __syncthreads();
-    if (lane == 0) { fs.g[wave * 4] = mx; fs.g[wave * 4 + 1] = mn; fs.g[wave * 4 + 2] = sm; }
-    __syncthreads();
-    mx = 0; mn = 0xffffffffu; sm = 0;
-    for (int w = 0; w < kFW; ++w) {
-      mx = max(mx, fs.g[w * 4]);
-      mn = min(mn, fs.g[w * 4 + 1]);
-      sm += fs.g[w * 4 + 2];
-    }
-    top = mx - 1u;
-    return sm == (uint32_t)V && mx > 0u && top < kInfKey && mn > kNegInfKey;
-  };
-
-  uint32_t top;
-  bool ok = survey(top);
-  const float m_raw = kval(top);
+  }
+  kmx = 0;
+  kmn = 0xffffffffu;
+  for (int w = 0; w < kFW; ++w) {
+    kmx = max(kmx, fs.g[w * 2]);
+    kmn = min(kmn, fs.g[w * 2 + 1]);
+  }
+  __syncthreads();
+  const uint32_t top_raw = kmx == 0x7fffu ? 0x8000u : kmx;  // -0 counts as +0
+  uint32_t top = top_raw;
+  bool ok = top_raw < kInfKey && kmn > kNegInfKey;  // non-finite rows take the multi-pass path
+  const float m_raw = kval(top_raw);
   float H_T = 0.f;
   if (ok && use_pen) {
     // Entropy of the raw values, then every penalised token (each distinct id once: the one
@@ -947,6 +948,8 @@ _Pragma("clang loop unroll(full)")
       if (atomicAnd(&pbits[id >> 5], ~bit) & bit) {
         const float x = RE::scalar(rp, id);
         const uint32_t kx = nkey(x), kp = nkey(pen_value(x));
+        if (kp >= kInfKey || kp <= kNegInfKey) atomicOr(&fs.bad, 1u);
+        atomicMax(&fs.top_pen, kp);
         if (kx != kp) {
           atomicSub(&hist[kx >> 1], 1u << ((kx & 1u) << 4));
           atomicAdd(&hist[kp >> 1], 1u << ((kp & 1u) << 4));
@@ -958,18 +961,34 @@ _Pragma("clang loop unroll(full)")
       const int id = p.pen_ids[j];
       if (id >= 0 && id < V) atomicOr(&pbits[id >> 5], 1u << (id & 31));
     }
+    // The largest value now: the raw one unless all its tokens moved (then the next value
+    // below it), or a moved token's.
+    const bool top_left = ((hist[top_raw >> 1] >> ((top_raw & 1u) * 16)) & 0xffffu) != 0;
+    if (!top_left && wave == 0) {
+      uint32_t best = 0;  // key + 1 of the largest value below top_raw; 0: none
+      for (int s2 = (int)(top_raw / kSlabBins); s2 >= 0; --s2) {
+        const uint2 wd = reinterpret_cast<const uint2*>(hist)[s2 * (kSlabBins / 4) + lane];
+_Pragma("clang loop unroll(full)")
+        for (int q = 0; q < 4; ++q) {
+          const uint32_t n = ((q < 2 ? wd.x : wd.y) >> ((q & 1) * 16)) & 0xffffu;
+          const uint32_t k = (uint32_t)(s2 * kSlabBins + lane * 4 + q);
+          if (n && k < top_raw) best = max(best, k + 1u);
+        }
+_Pragma("clang loop unroll(full)")
+        for (int o = 32; o >= 1; o >>= 1) best = max(best, (uint32_t)__shfl_xor(best, o));
+        if (best) break;
+      }
+      if (lane == 0) fs.sel[6] = best;
+    }
     __syncthreads();
-    ok = survey(top);
-  }
-  if (!ok) {
-    __syncthreads();
-    rows_generic<T, AL, kFT>(p, row, *reinterpret_cast<RowSharedT<kFW>*>(hist), pbits);
-    return;
+    top = max(top_left ? top_raw : (fs.sel[6] ? fs.sel[6] - 1u : 0u), fs.top_pen);
+    ok = fs.bad == 0;
   }
   const float m_pen = kval(top);
 
   // ---- resolution: one sweep over the slabs (wave w takes slabs w, w + 16, ...; lane l the
-  // four values 4l .. 4l + 3 of the slab) for the entropy sums, each slab's mass and count ----
+  // four values 4l .. 4l + 3 of the slab) for the entropy sums, each slab's mass and count, and
+  // the token total (a 16-bit count that overflowed leaves it short of V) ----
   const bool need_pen_sums = p.topk > 0 || p.out_entropy_pen != nullptr || p.out_lse != nullptr;
   const bool want_mass = p.do_sample != 0, want_cnt = p.topk > 0;
   auto unit_mass = [&](uint32_t k) __attribute__((always_inline)) -> uint64_t {
@@ -977,47 +996,62 @@ _Pragma("clang loop unroll(full)")
     return ys >= -41.0f ? det_q(ys) : 0;
   };
   float acc[4] = {0.f, 0.f, 0.f, 0.f};
-  for (int i = 0; i < kSlabs / kFW; ++i) {
-    const int s = wave + i * kFW;
-    const uint2 wd = reinterpret_cast<const uint2*>(hist)[s * (kSlabBins / 4) + lane];
-    uint64_t mass = 0;
-    uint32_t cnt = 0;
-    if (__any((wd.x | wd.y) != 0u)) {
-      if ((wd.x | wd.y) != 0u) {
+  if (ok) {
+    const uint2* h2 = reinterpret_cast<const uint2*>(hist);
+    uint32_t total = 0;
+    uint2 nxt = h2[wave * (kSlabBins / 4) + lane];
+    for (int i = 0; i < kSlabs / kFW; ++i) {
+      const int s = wave + i * kFW;
+      const uint2 wd = nxt;
+      if (i + 1 < kSlabs / kFW) nxt = h2[(s + kFW) * (kSlabBins / 4) + lane];  // next slab's read in flight
+      uint64_t mass = 0;
+      uint32_t cnt = 0;
+      if (__any((wd.x | wd.y) != 0u)) {
+        if ((wd.x | wd.y) != 0u) {
 _Pragma("clang loop unroll(full)")
-        for (int b = 0; b < 4; ++b) {
-          const uint32_t n = ((b < 2 ? wd.x : wd.y) >> ((b & 1) * 16)) & 0xffffu;
-          if (!n) continue;
-          const uint32_t k = (uint32_t)(s * kSlabBins + lane * 4 + b);
-          const float v = kval(k), fn = (float)n;
-          if (!use_pen) {
-            const float y = (v - m_raw) * p.ent_c;
-            const float e = fast_exp2(y);
-            acc[0] += fn * e;
-            acc[1] += e > 0.f ? fn * (e * y) : 0.f;
+          for (int b = 0; b < 4; ++b) {
+            const uint32_t n = ((b < 2 ? wd.x : wd.y) >> ((b & 1) * 16)) & 0xffffu;
+            if (!n) continue;
+            const uint32_t k = (uint32_t)(s * kSlabBins + lane * 4 + b);
+            const float v = kval(k), fn = (float)n;
+            if (!use_pen) {
+              const float y = (v - m_raw) * p.ent_c;
+              const float e = fast_exp2(y);
+              acc[0] += fn * e;
+              acc[1] += e > 0.f ? fn * (e * y) : 0.f;
+            }
+            if (need_pen_sums) {
+              const float y1 = (v - m_pen) * kLog2e;
+              const float e1 = fast_exp2(y1);
+              acc[2] += fn * e1;
+              acc[3] += e1 > 0.f ? fn * (e1 * y1) : 0.f;
+            }
+            if (want_mass) {
+              const float ys = (v - m_pen) * p.samp_c;
+              if (ys >= -41.0f) mass += (uint64_t)n * det_q(ys);
+            }
+            cnt += n;
           }
-          if (need_pen_sums) {
-            const float y1 = (v - m_pen) * kLog2e;
-            const float e1 = fast_exp2(y1);
-            acc[2] += fn * e1;
-            acc[3] += e1 > 0.f ? fn * (e1 * y1) : 0.f;
-          }
-          if (want_mass) {
-            const float ys = (v - m_pen) * p.samp_c;
-            if (ys >= -41.0f) mass += (uint64_t)n * det_q(ys);
-          }
-          cnt += n;
         }
+        total += cnt;
+        if (want_mass) mass = wave_sum_u64(mass);
+        if (want_cnt) cnt = wave_sum_u32(cnt);
       }
-      if (want_mass) mass = wave_sum_u64(mass);
-      if (want_cnt) cnt = wave_sum_u32(cnt);
+      if (lane == 0) {
+        fs.slab_mass[s] = mass;
+        fs.slab_cnt[s] = cnt;
+      }
     }
-    if (lane == 0) {
-      fs.slab_mass[s] = mass;
-      fs.slab_cnt[s] = cnt;
-    }
+    total = wave_sum_u32(total);
+    if (lane == 0) atomicAdd(&fs.total, total);
+    { const int op[4] = {1, 1, 1, 1}; block_reduce<4>(acc, op, fs); }
+    ok = fs.total == (uint32_t)V;
   }
-  { const int op[4] = {1, 1, 1, 1}; block_reduce<4>(acc, op, fs); }
+  if (!ok) {
+    __syncthreads();
+    rows_generic<T, AL, kFT>(p, row, *reinterpret_cast<RowSharedT<kFW>*>(hist), pbits);
+    return;
+  }
   if (!use_pen) H_T = (log2f(acc[0]) - acc[1] / acc[0]) * kLn2;
   const float H_pen = (log2f(acc[2]) - acc[3] / acc[2]) * kLn2;
   const float logsum = logf(acc[2]);
@@ -1029,115 +1063,131 @@ _Pragma("clang loop unroll(full)")
   }
   if (!p.do_sample && p.topk == 0) return;
 
-  // Slab holding position pos (largest keys first): thread t holds slab kSlabs - 1 - t with
-  // `mine` and the exclusive prefix `ex`.
-  auto find_slab = [&](uint64_t mine, uint64_t ex, uint64_t pos, uint64_t& above) __attribute__((always_inline)) -> int {
-    if (mine && ex <= pos && pos < ex + mine) {
-      fs.sel[0] = (uint32_t)(kSlabs - 1 - tid);
-      fs.sel64[0] = ex;
-    }
-    __syncthreads();
-    const int s = min((int)fs.sel[0], kSlabs - 1);  // pos is always inside the total
-    above = fs.sel64[0];
-    __syncthreads();
-    return s;
+  // Wave-level resolution (no barriers): the slab, then the value, holding position pos, keys
+  // descending. Lane l holds slabs kSlabs-1-4l .. kSlabs-4-4l (largest keys in lane 0).
+  auto rd64 = [](uint64_t v, int l) __attribute__((always_inline)) -> uint64_t {
+    return ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(v >> 32), l) << 32) |
+           (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, l);
   };
-  // Value holding position pos inside slab s (whose larger keys hold `above`), by sampler mass or
-  // by token count; wave 0 resolves it, every thread returns the key and the mass above it.
-  auto slab_pick = [&](int s, uint64_t above, uint64_t pos, bool by_mass, uint64_t& above_k) __attribute__((always_inline)) -> uint32_t {
-    if (wave == 0) {
-      const uint2 wd = reinterpret_cast<const uint2*>(hist)[s * (kSlabBins / 4) + lane];
-      uint64_t m[4], tot = 0;
+  auto wave_locate = [&](const uint64_t (&sm)[4], uint64_t ex, uint64_t lt, uint64_t pos, uint64_t& above) __attribute__((always_inline)) -> int {
+    const int L = __ffsll((unsigned long long)__ballot(lt != 0 && ex <= pos && pos < ex + lt)) - 1;
+    int slab = 0;
+    uint64_t run = ex, a = 0;
 _Pragma("clang loop unroll(full)")
-      for (int b = 0; b < 4; ++b) {
-        const uint32_t n = ((b < 2 ? wd.x : wd.y) >> ((b & 1) * 16)) & 0xffffu;
-        const uint32_t k = (uint32_t)(s * kSlabBins + lane * 4 + b);
-        m[b] = n == 0 ? 0 : by_mass ? (uint64_t)n * unit_mass(k) : (uint64_t)n;
-        tot += m[b];
-      }
-      uint64_t inc = tot;  // suffix sum: lanes above hold larger keys
-_Pragma("clang loop unroll(full)")
-      for (int o = 1; o < 64; o <<= 1) {
-        const uint64_t t = shfl_down_u64(inc, o);
-        if (lane + o < 64) inc += t;
-      }
-      uint64_t run = above + (inc - tot);
-_Pragma("clang loop unroll(full)")
-      for (int b = 3; b >= 0; --b) {
-        if (m[b] && run <= pos && pos < run + m[b]) {
-          fs.sel[1] = (uint32_t)(s * kSlabBins + lane * 4 + b);
-          fs.sel64[1] = run;
-        }
-        run += m[b];
-      }
+    for (int q = 0; q < 4; ++q) {
+      if (sm[q] != 0 && run <= pos && pos < run + sm[q]) { slab = kSlabs - 1 - (4 * lane + q); a = run; }
+      run += sm[q];
     }
-    __syncthreads();
-    const uint32_t k = fs.sel[1] & 0xffffu;
-    above_k = fs.sel64[1];
-    __syncthreads();
-    return k;
+    const int l = max(L, 0);  // pos is always inside the total
+    above = rd64(a, l);
+    return __builtin_amdgcn_readlane(slab, l);
+  };
+  auto wave_pick = [&](int s, uint64_t above, uint64_t pos, bool by_mass, uint64_t& above_k) __attribute__((always_inline)) -> uint32_t {
+    const uint2 wd = reinterpret_cast<const uint2*>(hist)[s * (kSlabBins / 4) + lane];
+    uint64_t m[4], tot = 0;
+_Pragma("clang loop unroll(full)")
+    for (int b = 0; b < 4; ++b) {
+      const uint32_t n = ((b < 2 ? wd.x : wd.y) >> ((b & 1) * 16)) & 0xffffu;
+      const uint32_t k = (uint32_t)(s * kSlabBins + lane * 4 + b);
+      m[b] = n == 0 ? 0 : by_mass ? (uint64_t)n * unit_mass(k) : (uint64_t)n;
+      tot += m[b];
+    }
+    uint64_t inc = tot;  // suffix sum: lanes above hold larger keys
+_Pragma("clang loop unroll(full)")
+    for (int o = 1; o < 64; o <<= 1) {
+      const uint64_t t = shfl_down_u64(inc, o);
+      if (lane + o < 64) inc += t;
+    }
+    uint64_t run = above + (inc - tot), a = 0;
+    uint32_t key = 0;
+    bool hit = false;
+_Pragma("clang loop unroll(full)")
+    for (int b = 3; b >= 0; --b) {
+      if (m[b] && run <= pos && pos < run + m[b]) {
+        key = (uint32_t)(s * kSlabBins + lane * 4 + b);
+        a = run;
+        hit = true;
+      }
+      run += m[b];
+    }
+    const int l = max(__ffsll((unsigned long long)__ballot(hit)) - 1, 0);
+    above_k = rd64(a, l);
+    return (uint32_t)__builtin_amdgcn_readlane((int)key, l);
+  };
+  // Per-lane slab values (4 slabs, largest keys first) and their exclusive prefix over lanes.
+  auto wave_slabs = [&](const uint64_t* src64, const uint32_t* src32, uint64_t (&sm)[4], uint64_t& lt) __attribute__((always_inline)) -> uint64_t {
+    lt = 0;
+_Pragma("clang loop unroll(full)")
+    for (int q = 0; q < 4; ++q) {
+      const int s = kSlabs - 1 - (4 * lane + q);
+      sm[q] = src64 ? src64[s] : (uint64_t)src32[s];
+      lt += sm[q];
+    }
+    uint64_t inc = lt;
+_Pragma("clang loop unroll(full)")
+    for (int o = 1; o < 64; o <<= 1) {
+      const uint64_t t = shfl_up_u64(inc, o);
+      if (lane >= o) inc += t;
+    }
+    return inc - lt;
   };
 
-  // ---- the draw: nucleus boundary, kept mass, r, the drawn value and its tie index ----
-  float v_r = 0.f;
-  uint32_t j_r = 0;
-  if (p.do_sample) {
-    const uint64_t mine = tid < kSlabs ? fs.slab_mass[kSlabs - 1 - tid] : 0;
-    uint64_t Z;
-    const uint64_t ex = block_excl_scan_u64(mine, Z, fs);
+  // ---- the draw (wave 0): nucleus boundary, kept mass, r, the drawn value and its tie index ----
+  if (p.do_sample && wave == 0) {
+    uint64_t sm[4], lt;
+    const uint64_t ex = wave_slabs(fs.slab_mass, nullptr, sm, lt);
+    const uint64_t Z = rd64(ex + lt, 63);
     uint64_t need = (uint64_t)(((unsigned __int128)Z * p.top_p_q32 + 0xffffffffull) >> 32);
     if (need < 1) need = 1;
     uint64_t a_s, above_n, above_r;
-    int s = find_slab(mine, ex, need - 1, a_s);
-    const uint32_t key_n = slab_pick(s, a_s, need - 1, true, above_n);
+    int s = wave_locate(sm, ex, lt, need - 1, a_s);
+    const uint32_t key_n = wave_pick(s, a_s, need - 1, true, above_n);
     const uint64_t qn = unit_mass(key_n);
     const uint64_t jn = (need - 1 - above_n) / qn;  // 0-based index of the last kept tie
     const uint64_t kept = above_n + (jn + 1) * qn;
-    uint32_t c4[4] = {(uint32_t)row, (uint32_t)p.step, (uint32_t)(p.step >> 32), 0u};
-    philox4x32_10(c4, (uint32_t)p.seed, (uint32_t)(p.seed >> 32));
-    const uint64_t U = ((uint64_t)c4[0] << 32) | c4[1];
     const uint64_t r = (uint64_t)(((unsigned __int128)U * kept) >> 64);
-    s = find_slab(mine, ex, r, a_s);
-    const uint32_t key_r = slab_pick(s, a_s, r, true, above_r);
-    j_r = (uint32_t)((r - above_r) / unit_mass(key_r));
-    v_r = kval(key_r);
-  }
-  // ---- top-K: candidates are the values whose log-prob is at least the K-th token's ----
-  float v_thr = __builtin_huge_valf();
-  if (p.topk > 0) {
-    const uint64_t mine = tid < kSlabs ? fs.slab_cnt[kSlabs - 1 - tid] : 0;
-    uint64_t tot, a_s, a_k;
-    const uint64_t ex = block_excl_scan_u64(mine, tot, fs);
-    const int s = find_slab(mine, ex, (uint64_t)(p.topk - 1), a_s);
-    const uint32_t kb = slab_pick(s, a_s, (uint64_t)(p.topk - 1), false, a_k);
-    const float lpK = RE::round((kval(kb) - m_pen) - logsum);
-    if (wave == 0) {
-      // log-probs fall with the value: walk down from kb while they still equal lpK
-      uint32_t lowest = kb;
-      for (int s2 = (int)(kb / kSlabBins); s2 >= 0; --s2) {
-        const uint2 wd = reinterpret_cast<const uint2*>(hist)[s2 * (kSlabBins / 4) + lane];
-        bool stop = false;
-_Pragma("clang loop unroll(full)")
-        for (int b = 0; b < 4; ++b) {
-          const uint32_t n = ((b < 2 ? wd.x : wd.y) >> ((b & 1) * 16)) & 0xffffu;
-          const uint32_t k = (uint32_t)(s2 * kSlabBins + lane * 4 + b);
-          if (n && k < kb) {
-            if (RE::round((kval(k) - m_pen) - logsum) == lpK) lowest = min(lowest, k);
-            else stop = true;
-          }
-        }
-        lowest = wave_min_u32(lowest);
-        if (__any(stop)) break;
-      }
-      if (lane == 0) fs.sel[2] = lowest;
+    s = wave_locate(sm, ex, lt, r, a_s);
+    const uint32_t key_r = wave_pick(s, a_s, r, true, above_r);
+    if (lane == 0) {
+      fs.sel[0] = key_r;
+      fs.sel[1] = (uint32_t)((r - above_r) / unit_mass(key_r));
     }
-    __syncthreads();
-    v_thr = kval(fs.sel[2]);
   }
+  // ---- top-K (wave 1): candidates are the values whose log-prob is at least the K-th token's ----
+  if (p.topk > 0 && wave == 1) {
+    uint64_t sm[4], lt, a_s, a_k;
+    const uint64_t ex = wave_slabs(nullptr, fs.slab_cnt, sm, lt);
+    const int s = wave_locate(sm, ex, lt, (uint64_t)(p.topk - 1), a_s);
+    const uint32_t kb = wave_pick(s, a_s, (uint64_t)(p.topk - 1), false, a_k);
+    const float lpK = RE::round((kval(kb) - m_pen) - logsum);
+    // log-probs fall with the value: walk down from kb while they still equal lpK
+    uint32_t lowest = kb;
+    for (int s2 = (int)(kb / kSlabBins); s2 >= 0; --s2) {
+      const uint2 wd = reinterpret_cast<const uint2*>(hist)[s2 * (kSlabBins / 4) + lane];
+      bool stop = false;
+_Pragma("clang loop unroll(full)")
+      for (int b = 0; b < 4; ++b) {
+        const uint32_t n = ((b < 2 ? wd.x : wd.y) >> ((b & 1) * 16)) & 0xffffu;
+        const uint32_t k = (uint32_t)(s2 * kSlabBins + lane * 4 + b);
+        if (n && k < kb) {
+          if (RE::round((kval(k) - m_pen) - logsum) == lpK) lowest = min(lowest, k);
+          else stop = true;
+        }
+      }
+      lowest = wave_min_u32(lowest);
+      if (__any(stop)) break;
+    }
+    if (lane == 0) fs.sel[2] = lowest;
+  }
+  __syncthreads();
+  const float v_r = p.do_sample ? kval(fs.sel[0] & 0xffffu) : 0.f;
+  const uint32_t j_r = p.do_sample ? fs.sel[1] : 0u;
+  const float v_thr = p.topk > 0 ? kval(fs.sel[2] & 0xffffu) : __builtin_huge_valf();
 
-  // ---- pass B (the row again): matches of the drawn value per (chunk, wave); top-K candidates ----
-  uint32_t* cnt = hist;                                      // [kFastChunks][kFW]
-  uint2* cand = reinterpret_cast<uint2*>(hist + 1024);       // [kCandCap] (log-prob bits, index)
+  // ---- pass B (the row again): each lane's 8-bit mask of tokens equal to the drawn value per
+  // chunk, and the top-K candidates ----
+  uint8_t* masks = reinterpret_cast<uint8_t*>(hist);         // [kFastChunks][kFW][64 lanes]
+  uint2* cand = reinterpret_cast<uint2*>(hist + 8192);       // [kCandCap] (log-prob bits, index)
   const float v_match = p.do_sample ? v_r : __builtin_nanf("");  // NaN matches nothing
   __syncthreads();
   if (tid == 0) fs.ncand = 0;
@@ -1149,23 +1199,19 @@ _Pragma("clang loop unroll(full)")
 _Pragma("clang loop unroll(full)")
     for (int u = 0; u < kRowUnroll; ++u) {
       const int c = c0 + u;
-      if (c >= nchunks) break;
+      if (c >= nchunks) continue;
       const int i0 = (c * kFT + tid) * EPV;
       const uint4 d = w[u];
       const uint32_t vm = i0 + EPV <= V ? 0xffu : i0 >= V ? 0u : (1u << (V - i0)) - 1u;  // valid elements
       const uint32_t pb = (use_pen && i0 < V) ? (pbits[i0 >> 5] >> (i0 & 31)) & vm & 0xffu : 0u;
       const uint32_t plain = vm & ~pb;
-      uint32_t m = 0, cm = 0;
+      uint32_t mt = 0, cm = 0;
 _Pragma("clang loop unroll(full)")
       for (int e = 0; e < EPV; ++e) {
         const float xv = RE::get(d, e);
         const bool pl = ((plain >> e) & 1u) != 0;
-        m += (pl && xv == v_match) ? 1u : 0u;
+        mt |= (pl && xv == v_match) ? 1u << e : 0u;
         cm |= (pl && xv >= v_thr) ? 1u << e : 0u;
-      }
-      if (p.do_sample) {
-        m = wave_sum_u32(m);
-        if (lane == 0) cnt[c * kFW + wave] = m;
       }
       // penalised elements and top-K candidates (both rare), one at a time
       for (uint32_t bits = pb | cm; bits != 0u; bits &= bits - 1u) {
@@ -1173,7 +1219,7 @@ _Pragma("clang loop unroll(full)")
         float xv = RE::get(d, e);
         if ((pb >> e) & 1u) {
           xv = pen_value(xv);
-          if (xv == v_match) atomicAdd(&cnt[c * kFW + wave], 1u);
+          if (xv == v_match) mt |= 1u << e;
           if (!(xv >= v_thr)) continue;
         }
         if (p.topk > 0) {
@@ -1182,6 +1228,7 @@ _Pragma("clang loop unroll(full)")
             cand[pos] = make_uint2(__float_as_uint(RE::round((xv - m_pen) - logsum)), (uint32_t)(i0 + e));
         }
       }
+      if (p.do_sample) masks[(c * kFW + wave) * 64 + lane] = (uint8_t)mt;
     }
   }
   __syncthreads();
@@ -1254,44 +1301,50 @@ _Pragma("clang loop unroll(full)")
     }
   }
 
-  // ---- the drawn token: the j_r-th (by index) token of value v_r ----
+  // ---- the drawn token: the j_r-th (by index) token of value v_r. Thread t takes the masks of
+  // (chunk t / 16, wave t % 16), whose tokens follow in index order (lane, then element) ----
   if (p.do_sample) {
-    const uint32_t v = tid < nchunks * kFW ? cnt[tid] : 0u;
-    if (tid == 0) fs.sel[3] = 0xffffffffu;
+    const int t = tid;
+    uint4 mw[4] = {};
+    uint32_t v = 0;
+    if (t < nchunks * kFW) {
+_Pragma("clang loop unroll(full)")
+      for (int q = 0; q < 4; ++q) {
+        mw[q] = reinterpret_cast<const uint4*>(masks + t * 64)[q];
+        v += __builtin_popcount(mw[q].x) + __builtin_popcount(mw[q].y) + __builtin_popcount(mw[q].z) +
+             __builtin_popcount(mw[q].w);
+      }
+    }
     uint64_t tot;
     const uint64_t ex = block_excl_scan_u64((uint64_t)v, tot, fs);
     if (v && ex <= j_r && j_r < ex + v) {
-      fs.sel[3] = (uint32_t)tid;
-      fs.sel64[3] = ex;
-    }
-    __syncthreads();
-    const uint32_t t = fs.sel[3];
-    if (t != 0xffffffffu && wave == (int)(t % kFW)) {
-      const int cs = (int)(t / kFW);
-      const uint4 d = load_raw(cs);
-      const int i0 = (cs * kFT + tid) * EPV;
-      const uint32_t pb = (use_pen && i0 < V) ? (pbits[i0 >> 5] >> (i0 & 31)) & 0xffu : 0u;
-      uint32_t mt = 0;  // bit e: element e matches
-      for (int e = 0; e < EPV; ++e) {
-        float xv = RE::get(d, e);
-        if ((pb >> e) & 1u) xv = pen_value(xv);
-        if (i0 + e < V && xv == v_r) mt |= 1u << e;
-      }
-      const uint32_t m = (uint32_t)__builtin_popcount(mt);
-      uint32_t inc = m;
-      for (int o = 1; o < 64; o <<= 1) {
-        const uint32_t u = __shfl_up(inc, o);
-        if (lane >= o) inc += u;
-      }
-      uint32_t seen = (uint32_t)fs.sel64[3] + inc - m;
-      if (m && seen <= j_r && j_r < seen + m) {
-        for (int e = 0; e < EPV; ++e) {
-          if ((mt >> e) & 1u) {
-            if (seen == j_r && p.out_sample) p.out_sample[row] = i0 + e;
-            ++seen;
+      // the 16 words of lane masks (4 lanes each): popcounts, then the word, byte and bit
+      // holding match j_r (static selections: no dynamic register indexing)
+      const uint32_t wv[16] = {mw[0].x, mw[0].y, mw[0].z, mw[0].w, mw[1].x, mw[1].y, mw[1].z, mw[1].w,
+                               mw[2].x, mw[2].y, mw[2].z, mw[2].w, mw[3].x, mw[3].y, mw[3].z, mw[3].w};
+      uint32_t seen = (uint32_t)ex, wsel = 0, base = 0;
+      int wi_found = -1;
+      static_for<16>([&](auto wi_) __attribute__((always_inline)) {
+        constexpr int wi = decltype(wi_)::value;
+        const uint32_t n = (uint32_t)__builtin_popcount(wv[wi]);
+        if (wi_found < 0 && seen + n > j_r) { wi_found = wi; wsel = wv[wi]; base = seen; }
+        seen += n;
+      });
+      int found = -1;
+      if (wi_found >= 0) {
+        static_for<4>([&](auto bb_) __attribute__((always_inline)) {
+          constexpr int bb = decltype(bb_)::value;
+          uint32_t mb = (wsel >> (8 * bb)) & 0xffu;
+          const uint32_t n = (uint32_t)__builtin_popcount(mb);
+          if (found < 0 && base + n > j_r) {
+            for (uint32_t r = j_r - base; r > 0; --r) mb &= mb - 1u;  // drop the earlier matches
+            found = (wi_found * 4 + bb) * EPV + __builtin_ctz(mb);      // lane * 8 + element
           }
-        }
+          base += n;
+        });
       }
+      if (found >= 0 && p.out_sample)
+        p.out_sample[row] = ((t / kFW) * kFT + (t % kFW) * 64) * EPV + found;
     }
   }
 }
