@@ -38,12 +38,13 @@ METRIC = "branch-decode tokens/sec on 1 GPU; paged-decode achieved HBM GB/s vs p
 PEAK_HBM_GBS = 8000.0
 PEAK_BF16_TFLOPS = 2500.0  # dense bf16 MFMA
 TRAFFIC_FILE = os.path.join(HERE, "profiles", "paged_decode_llama3_8b_traffic.txt")
+ROWS_TRAFFIC_FILE = os.path.join(HERE, "profiles", "row_stats_sampling.md")
 
 
-def _measured_traffic():
-    """HBM bytes per decode launch from the committed rocprofv3 --pmc summary, if any."""
+def _measured_traffic(path: str = TRAFFIC_FILE):
+    """HBM bytes per launch from a committed rocprofv3 --pmc summary, if any."""
     try:
-        text = open(TRAFFIC_FILE).read()
+        text = open(path).read()
     except OSError:
         return None
     m = re.search(r"^traffic_bytes_per_launch:\s*([0-9.eE+]+)", text, flags=re.M)
@@ -301,10 +302,23 @@ def run_rows(args, dev) -> dict:
     # cannot hold a step's 78 MB until the next time it is read.
     xs = [x] + [sampling_logits(device=dev, seed=s)[0] for s in (1, 2, 3)]
     state = {"i": 0}
+    # One launch of the fused kernel per step through the C ABI, into outputs allocated once
+    # (ops.row_stats would add their allocation and a fill of the sample ids).
+    from mentat_amd._lib import get_lib, stream_handle
+
+    lib = get_lib()
+    ent = torch.empty(R, dtype=torch.float32, device=dev)
+    gate = torch.empty(R, dtype=torch.uint8, device=dev)
+    smp = torch.empty(R, dtype=torch.int32, device=dev)
+    sh = stream_handle(dev)
 
     def step():
-        ops.row_stats(xs[state["i"] % len(xs)], temperature=T, gate_threshold=THR, sample=True,
-                      sample_temperature=T, top_p=TOP_P, seed=1234, step=state["i"], pen_stats=False)
+        xi = xs[state["i"] % len(xs)]
+        st = lib.mentat_row_stats(xi.data_ptr(), xi.stride(0), R, V, 2, T, 1.0, None, None, THR, 0, 1, T, TOP_P,
+                                  1234, state["i"], ent.data_ptr(), None, None, gate.data_ptr(), None, None,
+                                  smp.data_ptr(), sh)
+        if st != 0:
+            raise RuntimeError(f"mentat_row_stats returned {st}")
         state["i"] += 1
 
     ms = _time_steps(step, args.steps, args.warmup, dev)
@@ -335,7 +349,8 @@ def run_rows(args, dev) -> dict:
         "rotation": "4 logits sets (seeds 0-3) used in turn",
         "logits_bytes_per_step": nbytes,
     }
-    line = _line(args, nbytes / (ms * 1e-3) / 1e9, ms, config, cpu, None, {"rows_per_s": round(R * 1e3 / ms, 1)})
+    line = _line(args, nbytes / (ms * 1e-3) / 1e9, ms, config, cpu, _measured_traffic(ROWS_TRAFFIC_FILE),
+                 {"rows_per_s": round(R * 1e3 / ms, 1)})
     line["data"] = "synthetic (seeded N(0, sigma_r) logits)"
     return line
 
