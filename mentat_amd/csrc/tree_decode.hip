@@ -85,7 +85,7 @@ struct TreeParams {
 
 constexpr int kTreeWaves = 8;
 constexpr int kTreeThreads = 64 * kTreeWaves;
-constexpr int kTreePrefetch = 8;        // shared path: tiles in flight per loading thread (even)
+constexpr int kTreePrefetch = 4;        // shared path: tiles in flight per loading thread (even)
 constexpr int kTreeSharedMaxTiles = 16;  // shared path: tiles per task (host-enforced)
 constexpr float kTreeSlack = 8.f;
 
