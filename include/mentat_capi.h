@@ -187,6 +187,36 @@ int mentat_semantic_similar(const int64_t* ptrs, const int32_t* parent_key, cons
                             void* stream);
 
 /* ------------------------------------------------------------------------
+ * Per-layer glue of the captured decode step (16-bit models; dtype
+ * MENTAT_BF16 or MENTAT_F16). The reference's decode loop
+ * (core/generator_utils.py:340-418) runs each layer with the model's own
+ * modules: input_layernorm, RoPE in the adapters' rotate_half form
+ * (adapters/llama_adapter.py:70-113), post_attention_layernorm, the MLP and
+ * two residual adds. Each entry point is one launch and rounds as the torch
+ * kernels it replaces (one rounding to the dtype per torch op).
+ *
+ * mentat_rmsnorm: for each of `rows` rows of H elements (H % 8 == 0,
+ * H <= 8192, 16-byte aligned buffers): h = x, or h = rnd(residual_in + x)
+ * written to residual_out when residual_in is given; then
+ * out = rnd(weight * rnd(h * rsqrt(mean(h^2) + eps))) (HF LlamaRMSNorm /
+ * Qwen3RMSNorm). The fp32 summation order of the mean differs from torch's.
+ *
+ * mentat_rope: in place on q [rows][Hq][D] and k [rows][Hk][D] with cos/sin
+ * [rows][D]: t = rnd(rnd(t * cos) + rnd(rotate_half(t) * sin)).
+ *
+ * mentat_silu_mul: out = rnd(rnd(silu(gate)) * up) over n elements
+ * (n % 8 == 0, 16-byte aligned), silu(g) = g / (1 + exp(-g)) in fp32
+ * (the LlamaMLP / Qwen3MLP activation and product).
+ * ------------------------------------------------------------------------ */
+int mentat_rmsnorm(const void* x, const void* residual_in, void* residual_out, const void* weight, void* out,
+                   int rows, int H, float eps, int dtype, void* stream);
+
+int mentat_rope(void* q, void* k, const void* cos, const void* sin, int rows, int Hq, int Hk, int D, int dtype,
+                void* stream);
+
+int mentat_silu_mul(const void* gate, const void* up, void* out, int64_t n, int dtype, void* stream);
+
+/* ------------------------------------------------------------------------
  * KV append: write n new token rows into the pools, fused with the lazy
  * copy-on-write of a shared tail page and the device block-table update.
  *

@@ -71,6 +71,21 @@ SIGNATURES: dict[str, tuple] = {
             _c_int, _c_float, _c_int, _c_void_p,  # window, scale, dtype, stream
         ],
     ),
+    "mentat_rmsnorm": (
+        _c_int,
+        [
+            _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,  # x, residual_in, residual_out, weight, out
+            _c_int, _c_int, _c_float, _c_int, _c_void_p,  # rows, H, eps, dtype, stream
+        ],
+    ),
+    "mentat_rope": (
+        _c_int,
+        [
+            _c_void_p, _c_void_p, _c_void_p, _c_void_p,  # q, k, cos, sin
+            _c_int, _c_int, _c_int, _c_int, _c_int, _c_void_p,  # rows, Hq, Hk, D, dtype, stream
+        ],
+    ),
+    "mentat_silu_mul": (_c_int, [_c_void_p, _c_void_p, _c_void_p, _c_i64, _c_int, _c_void_p]),
     "mentat_semantic_ema": (
         _c_int,
         [

@@ -28,6 +28,12 @@ K/V stores, of its own input buffer and of the paged-decode workspace, so
 Warm-up and capture run with an all-padding input, which writes nothing to
 the cache.
 
+For 16-bit HF Llama/Qwen3-style models whose adapter keeps the stock glue, the
+captured layer also fuses that glue: each residual add with the RMSNorm that
+follows it (across the layer boundary too), RoPE of Q and K in one launch, and
+SiLU(gate) * up (ops.rmsnorm, ops.rope_, ops.silu_mul); other models run their
+modules as they are.
+
 No object is destroyed while a capture is active: the garbage collector runs
 just before each capture and stays disabled during it. (A finished run's
 graphs, pools and pinned buffers, if left to the cyclic collector, could
@@ -45,6 +51,7 @@ import torch
 
 from .. import ops
 from .._lib import get_lib
+from ..adapters.model_adapter import _HFDecoderAdapter
 
 __all__ = ["DecodeGraphs", "BUCKETS"]
 
@@ -55,6 +62,31 @@ __all__ = ["DecodeGraphs", "BUCKETS"]
 # 7.2 ms for 160, 6.1 ms for 184 but 8.2 ms for 192. The buckets skip those
 # row counts and step by 16 where the cost rises with the rows.
 BUCKETS = (8, 16, 32, 48, 64, 80, 88, 104, 120, 136, 152, 168, 184, 200, 216, 232, 248, 256)
+
+
+def _fusable(a, dtype) -> bool:
+    """The captured step may fuse the layer glue: stock adapter hooks, HF RMSNorms
+    (weight + variance_epsilon), a SiLU-gated MLP, a 16-bit dtype."""
+    if dtype not in (torch.bfloat16, torch.float16) or not isinstance(a, _HFDecoderAdapter):
+        return False
+    for name in ("apply_pre_attn_norm", "apply_pre_mlp_norm", "apply_post_attn_residual", "apply_post_mlp_residual",
+                 "apply_rope", "get_mlp", "final_norm"):
+        if getattr(type(a), name) is not getattr(_HFDecoderAdapter, name):
+            return False
+
+    def norm_ok(n):
+        w = getattr(n, "weight", None)
+        return (w is not None and hasattr(n, "variance_epsilon") and w.dim() == 1 and w.dtype == dtype
+                and w.numel() % 8 == 0 and w.numel() <= 8192)
+
+    for block in a.layers:
+        mlp = block.mlp
+        act = getattr(mlp, "act_fn", None)
+        if not (norm_ok(block.input_layernorm) and norm_ok(block.post_attention_layernorm)
+                and all(hasattr(mlp, n) for n in ("gate_proj", "up_proj", "down_proj"))
+                and "silu" in type(act).__name__.lower()):
+            return False
+    return norm_ok(a.final_norm)
 
 
 class _Bucket:
@@ -74,6 +106,7 @@ class DecodeGraphs:
         self._stream = torch.cuda.Stream(self.dev)
         self._ws = None
         self.captures = 0
+        self.fused = _fusable(self.a, self.m.dtype)
 
     # ------------------------------------------------------------------
     def bucket(self, n: int):
@@ -109,6 +142,8 @@ class DecodeGraphs:
         plans[:, 6, n:] = 0
 
     def _forward(self, buf: torch.Tensor, nb: int):
+        if self.fused:
+            return self._forward_fused(buf, nb)
         a, m = self.a, self.m
         L = m.num_layers
         ids = buf[0:nb].long().unsqueeze(0)            # [1, nb]
@@ -137,6 +172,41 @@ class DecodeGraphs:
             hidden = a.apply_post_mlp_residual(block, residual, a.get_mlp(block)(x))
         hidden = a.final_norm(hidden).squeeze(0)
         return a.lm_head(hidden), hidden
+
+    def _forward_fused(self, buf: torch.Tensor, nb: int):
+        """_forward with the layer glue fused (see the module docstring)."""
+        a, m = self.a, self.m
+        L = m.num_layers
+        ids = buf[0:nb].long().unsqueeze(0)
+        pos = buf[nb:2 * nb].long().unsqueeze(1)
+        rows = buf[2 * nb:3 * nb]
+        plans = buf[3 * nb:].view(L, 7, nb)
+        max_seqlen = m._pages_cap * m.block_size
+        layers = a.layers
+        hidden = a.embeddings(ids)                     # [1, nb, H]: the residual stream
+        ln = layers[0].input_layernorm
+        x, _ = ops.rmsnorm(hidden, ln.weight, ln.variance_epsilon)
+        for layer_idx, block in enumerate(layers):
+            attn = a.get_self_attn(block)
+            q, k, v = a.project_qkv(attn, x.squeeze(0).unsqueeze(1))  # one token per sequence
+            cos, sin = a._build_cos_sin(pos, q)
+            q, k = q.contiguous(), k.contiguous()
+            ops.rope_(q, k, cos, sin)
+            ops.kv_append(k.squeeze(1).to(m.dtype).contiguous(), v.squeeze(1).to(m.dtype).contiguous(),
+                          m._k_store, m._v_store, plans[layer_idx], block_size=m.block_size, layout=m.layout,
+                          block_tables=m._tables[layer_idx], seq_lens=m._lens[layer_idx])
+            o = ops.paged_decode(q.squeeze(1), m._k_store, m._v_store, layout=m.layout,
+                                 block_tables=m._tables[layer_idx], seq_lens=m._lens[layer_idx], seq_rows=rows,
+                                 max_seqlen=max_seqlen)
+            attn_out = attn.o_proj(o.reshape(1, nb, -1))
+            ln = block.post_attention_layernorm
+            x, hidden = ops.rmsnorm(attn_out, ln.weight, ln.variance_epsilon, residual=hidden)
+            mlp = block.mlp
+            mlp_out = mlp.down_proj(ops.silu_mul(mlp.gate_proj(x), mlp.up_proj(x)))
+            ln = layers[layer_idx + 1].input_layernorm if layer_idx + 1 < L else a.final_norm
+            x, hidden = ops.rmsnorm(mlp_out, ln.weight, ln.variance_epsilon, residual=hidden)
+        x = x.squeeze(0)
+        return a.lm_head(x), x
 
     def _workspace(self) -> None:
         """Size the capture stream's decode workspace for the largest bucket."""

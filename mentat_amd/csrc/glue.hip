@@ -1,0 +1,231 @@
+// Fused per-layer glue of the captured decode step (gfx950), 16-bit models:
+// residual add + RMSNorm, rotary embedding of Q and K, SiLU(gate) * up.
+//
+// Reference: the decode loop of core/generator_utils.py:340-418 runs each
+// layer as input_layernorm -> q/k/v projections -> RoPE (the adapters'
+// rotate_half form, adapters/llama_adapter.py:70-113) -> attention -> o_proj
+// -> residual add -> post_attention_layernorm -> MLP -> residual add, with
+// the model's own modules (HF LlamaRMSNorm / Qwen3RMSNorm, LlamaMLP), each a
+// handful of torch kernels. Here each group is one launch, rounding as those
+// torch kernels do (one rounding to the tensor dtype per torch op):
+//   add:     h = rnd(residual + x)
+//   RMSNorm: y = rnd(w * rnd(h * rsqrt(mean(h^2) + eps)))   (h in fp32)
+//   RoPE:    t' = rnd(rnd(t * cos) + rnd(rotate_half(t) * sin))
+//   MLP act: m = rnd(rnd(silu(g)) * u),  silu(g) = g / (1 + exp(-g)) in fp32
+// Only the fp32 summation order of the norm's mean differs from torch.
+#include "mentat_common.h"
+
+namespace mentat {
+
+namespace {
+
+template <typename T> struct G16;
+template <> struct G16<BF16> {
+  __device__ static float lo(uint32_t w) { return bf16_lo(w); }
+  __device__ static float hi(uint32_t w) { return bf16_hi(w); }
+  __device__ static uint32_t bits(float v) { return f32_to_bf16(v); }
+  __device__ static float rnd(float v) { return __uint_as_float((uint32_t)f32_to_bf16(v) << 16); }
+};
+// The empty asm makes the float value exist before it is narrowed (no fused
+// mixed-precision instruction that would round once).
+template <> struct G16<F16> {
+  __device__ static float lo(uint32_t w) { return f16_bits_to_f32((uint16_t)(w & 0xffffu)); }
+  __device__ static float hi(uint32_t w) { return f16_bits_to_f32((uint16_t)(w >> 16)); }
+  __device__ static uint32_t bits(float v) {
+    asm volatile("" : "+v"(v));
+    return f32_to_f16_bits(v);
+  }
+  __device__ static float rnd(float v) {
+    asm volatile("" : "+v"(v));
+    return f16_bits_to_f32(f32_to_f16_bits(v));
+  }
+};
+
+constexpr int kNormThreads = 256;
+
+// One workgroup per row; each thread owns 8-element groups g = tid, tid + 256, ...
+// (H % 8 == 0, H <= 8 * 256 * kNormGroups).
+constexpr int kNormGroups = 4;
+template <typename T>
+__global__ __launch_bounds__(kNormThreads) void rmsnorm_kernel(const uint16_t* x, const uint16_t* res_in,
+                                                               uint16_t* res_out, const uint16_t* w, uint16_t* y,
+                                                               int H, float eps) {
+  using E = G16<T>;
+  const int row = blockIdx.x, tid = threadIdx.x;
+  const long base = (long)row * H;
+  const int ng = H / 8;
+  float h[kNormGroups][8];
+  float ss = 0.f;
+#pragma unroll
+  for (int k = 0; k < kNormGroups; ++k) {
+    const int g = tid + k * kNormThreads;
+    if (g < ng) {
+      const uint4 xv = *(const uint4*)(x + base + 8 * g);
+      const uint32_t xs[4] = {xv.x, xv.y, xv.z, xv.w};
+      if (res_in) {
+        const uint4 rv = *(const uint4*)(res_in + base + 8 * g);
+        const uint32_t rs[4] = {rv.x, rv.y, rv.z, rv.w};
+        uint32_t o[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          h[k][2 * j] = E::rnd(E::lo(rs[j]) + E::lo(xs[j]));
+          h[k][2 * j + 1] = E::rnd(E::hi(rs[j]) + E::hi(xs[j]));
+          o[j] = E::bits(h[k][2 * j]) | (E::bits(h[k][2 * j + 1]) << 16);
+        }
+        *(uint4*)(res_out + base + 8 * g) = make_uint4(o[0], o[1], o[2], o[3]);
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          h[k][2 * j] = E::lo(xs[j]);
+          h[k][2 * j + 1] = E::hi(xs[j]);
+        }
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ss = __builtin_fmaf(h[k][e], h[k][e], ss);
+    }
+  }
+  __shared__ float red[kNormThreads / 64];
+  for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
+  if ((tid & 63) == 0) red[tid >> 6] = ss;
+  __syncthreads();
+  float tot = 0.f;
+#pragma unroll
+  for (int i = 0; i < kNormThreads / 64; ++i) tot += red[i];
+  const float r = __frsqrt_rn(tot / (float)H + eps);
+#pragma unroll
+  for (int k = 0; k < kNormGroups; ++k) {
+    const int g = tid + k * kNormThreads;
+    if (g < ng) {
+      const uint4 wv = *(const uint4*)(w + 8 * g);
+      const uint32_t ws[4] = {wv.x, wv.y, wv.z, wv.w};
+      uint32_t o[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float a = E::rnd(E::lo(ws[j]) * E::rnd(h[k][2 * j] * r));
+        const float b = E::rnd(E::hi(ws[j]) * E::rnd(h[k][2 * j + 1] * r));
+        o[j] = E::bits(a) | (E::bits(b) << 16);
+      }
+      *(uint4*)(y + base + 8 * g) = make_uint4(o[0], o[1], o[2], o[3]);
+    }
+  }
+}
+
+// Rotary embedding in place on q [rows][Hq][D] and k [rows][Hk][D] with
+// cos/sin [rows][D]: one thread per (row, head, i < D/2) rotates the pair
+// (i, i + D/2). Grid: rows x ceil((Hq + Hk) * D/2 / 256).
+template <typename T>
+__global__ __launch_bounds__(256) void rope_kernel(uint16_t* q, uint16_t* k, const uint16_t* cs, const uint16_t* sn,
+                                                   int Hq, int Hk, int D) {
+  using E = G16<T>;
+  const int row = blockIdx.x;
+  const int half = D / 2;
+  const int idx = blockIdx.y * 256 + threadIdx.x;
+  if (idx >= (Hq + Hk) * half) return;
+  const int hd = idx / half, i = idx - hd * half;
+  uint16_t* t = hd < Hq ? q + ((long)row * Hq + hd) * D : k + ((long)row * Hk + (hd - Hq)) * D;
+  auto ld = [](const uint16_t* p, int j) { return E::lo((uint32_t)p[j]); };
+  const uint16_t* c = cs + (long)row * D;
+  const uint16_t* s = sn + (long)row * D;
+  const float a = ld(t, i), b = ld(t, i + half);
+  const float ya = E::rnd(E::rnd(a * ld(c, i)) + E::rnd(-b * ld(s, i)));
+  const float yb = E::rnd(E::rnd(b * ld(c, i + half)) + E::rnd(a * ld(s, i + half)));
+  t[i] = (uint16_t)E::bits(ya);
+  t[i + half] = (uint16_t)E::bits(yb);
+}
+
+// m = rnd(rnd(silu(g)) * u) over n elements (n % 8 == 0), 8 per thread.
+template <typename T>
+__global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t* g, const uint16_t* u, uint16_t* m, long n8) {
+  using E = G16<T>;
+  const long i = (long)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n8) return;
+  const uint4 gv = *(const uint4*)(g + 8 * i), uv = *(const uint4*)(u + 8 * i);
+  const uint32_t gs[4] = {gv.x, gv.y, gv.z, gv.w}, us[4] = {uv.x, uv.y, uv.z, uv.w};
+  uint32_t o[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const float g0 = E::lo(gs[j]), g1 = E::hi(gs[j]);
+    const float a = E::rnd(E::rnd(g0 / (1.f + expf(-g0))) * E::lo(us[j]));
+    const float b = E::rnd(E::rnd(g1 / (1.f + expf(-g1))) * E::hi(us[j]));
+    o[j] = E::bits(a) | (E::bits(b) << 16);
+  }
+  *(uint4*)(m + 8 * i) = make_uint4(o[0], o[1], o[2], o[3]);
+}
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+}  // namespace
+
+}  // namespace mentat
+
+using namespace mentat;
+
+extern "C" int mentat_rmsnorm(const void* x, const void* residual_in, void* residual_out, const void* weight, void* out,
+                              int rows, int H, float eps, int dtype, void* stream) {
+  if (rows < 0 || H <= 0) return MENTAT_EINVAL;
+  if (rows == 0) return MENTAT_OK;
+  if (!x || !weight || !out || (residual_in && !residual_out)) return MENTAT_EINVAL;
+  if (H % 8 != 0 || H > 8 * kNormThreads * kNormGroups) return MENTAT_EUNSUP;
+  if (!aligned16(x) || !aligned16(weight) || !aligned16(out) || (residual_in && (!aligned16(residual_in) ||
+                                                                               !aligned16(residual_out))))
+    return MENTAT_EINVAL;
+  hipStream_t s = (hipStream_t)stream;
+  const auto* xi = (const uint16_t*)x;
+  const auto* ri = (const uint16_t*)residual_in;
+  auto* ro = (uint16_t*)residual_out;
+  const auto* wi = (const uint16_t*)weight;
+  auto* yo = (uint16_t*)out;
+  switch (dtype) {
+    case MENTAT_BF16:
+      hipLaunchKernelGGL(rmsnorm_kernel<BF16>, dim3(rows), dim3(kNormThreads), 0, s, xi, ri, ro, wi, yo, H, eps);
+      break;
+    case MENTAT_F16:
+      hipLaunchKernelGGL(rmsnorm_kernel<F16>, dim3(rows), dim3(kNormThreads), 0, s, xi, ri, ro, wi, yo, H, eps);
+      break;
+    default:
+      return MENTAT_EUNSUP;
+  }
+  return (int)hipGetLastError();
+}
+
+extern "C" int mentat_rope(void* q, void* k, const void* cos, const void* sin, int rows, int Hq, int Hk, int D,
+                           int dtype, void* stream) {
+  if (rows < 0 || Hq < 0 || Hk < 0 || D <= 0 || D % 2 != 0) return MENTAT_EINVAL;
+  if (rows == 0 || Hq + Hk == 0) return MENTAT_OK;
+  if ((Hq && !q) || (Hk && !k) || !cos || !sin) return MENTAT_EINVAL;
+  hipStream_t s = (hipStream_t)stream;
+  const dim3 grid(rows, ((Hq + Hk) * (D / 2) + 255) / 256);
+  auto* qo = (uint16_t*)q;
+  auto* ko = (uint16_t*)k;
+  const auto* c = (const uint16_t*)cos;
+  const auto* sn = (const uint16_t*)sin;
+  switch (dtype) {
+    case MENTAT_BF16: hipLaunchKernelGGL(rope_kernel<BF16>, grid, dim3(256), 0, s, qo, ko, c, sn, Hq, Hk, D); break;
+    case MENTAT_F16: hipLaunchKernelGGL(rope_kernel<F16>, grid, dim3(256), 0, s, qo, ko, c, sn, Hq, Hk, D); break;
+    default: return MENTAT_EUNSUP;
+  }
+  return (int)hipGetLastError();
+}
+
+extern "C" int mentat_silu_mul(const void* gate, const void* up, void* out, int64_t n, int dtype, void* stream) {
+  if (n < 0) return MENTAT_EINVAL;
+  if (n == 0) return MENTAT_OK;
+  if (!gate || !up || !out) return MENTAT_EINVAL;
+  if (n % 8 != 0 || !aligned16(gate) || !aligned16(up) || !aligned16(out)) return MENTAT_EUNSUP;
+  hipStream_t s = (hipStream_t)stream;
+  const long n8 = n / 8;
+  const dim3 grid((unsigned)((n8 + 255) / 256));
+  switch (dtype) {
+    case MENTAT_BF16:
+      hipLaunchKernelGGL(silu_mul_kernel<BF16>, grid, dim3(256), 0, s, (const uint16_t*)gate, (const uint16_t*)up,
+                         (uint16_t*)out, n8);
+      break;
+    case MENTAT_F16:
+      hipLaunchKernelGGL(silu_mul_kernel<F16>, grid, dim3(256), 0, s, (const uint16_t*)gate, (const uint16_t*)up,
+                         (uint16_t*)out, n8);
+      break;
+    default:
+      return MENTAT_EUNSUP;
+  }
+  return (int)hipGetLastError();
+}

@@ -225,6 +225,61 @@ def prefill_attention(
     return out
 
 
+_GLUE_DTYPES = (torch.bfloat16, torch.float16)
+
+
+def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float, residual: Optional[torch.Tensor] = None):
+    """HF RMSNorm of the rows of ``x`` (last dim H), or of ``residual + x``
+    when ``residual`` is given (the residual add fused in). Returns
+    ``(out, h)`` with h = residual + x (None without a residual). 16-bit
+    dtypes; torch's rounding per op (mentat_rmsnorm)."""
+    _require(x.dtype in _GLUE_DTYPES and weight.dtype == x.dtype, "rmsnorm takes bf16/f16 x and weight")
+    _require(x.is_contiguous() and weight.is_contiguous() and weight.dim() == 1, "contiguous x and 1-d weight")
+    H = x.shape[-1]
+    _require(weight.numel() == H, "weight length must match the last dim")
+    rows = x.numel() // H
+    out = torch.empty_like(x)
+    h = None
+    if residual is not None:
+        _require(residual.shape == x.shape and residual.dtype == x.dtype and residual.is_contiguous(),
+                 "residual must match x")
+        h = torch.empty_like(x)
+    st = get_lib().mentat_rmsnorm(ptr(x), ptr(residual), ptr(h), ptr(weight), ptr(out), rows, H, float(eps),
+                                  DTYPE_CODES[x.dtype], stream_handle(x.device))
+    check(st, "mentat_rmsnorm")
+    return out, h
+
+
+def rope_(q: torch.Tensor, k: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> None:
+    """Rotary embedding in place: q [..., Hq, D] and k [..., Hk, D] (same
+    leading rows), cos/sin with D trailing elements per row;
+    t = t*cos + rotate_half(t)*sin with torch's rounding (mentat_rope)."""
+    _require(q.dtype in _GLUE_DTYPES and k.dtype == q.dtype and cos.dtype == q.dtype and sin.dtype == q.dtype,
+             "rope takes bf16/f16 tensors of one dtype")
+    _require(q.is_contiguous() and k.is_contiguous() and cos.is_contiguous() and sin.is_contiguous(),
+             "rope takes contiguous tensors")
+    D = q.shape[-1]
+    rows = cos.numel() // D
+    _require(sin.numel() == rows * D and q.numel() % (rows * D) == 0 and k.numel() % (rows * D) == 0,
+             "q, k, cos and sin must share the leading rows")
+    Hq, Hk = q.numel() // (rows * D), k.numel() // (rows * D)
+    st = get_lib().mentat_rope(ptr(q), ptr(k), ptr(cos), ptr(sin), rows, Hq, Hk, D, DTYPE_CODES[q.dtype],
+                               stream_handle(q.device))
+    check(st, "mentat_rope")
+
+
+def silu_mul(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
+    """silu(gate) * up with torch's rounding per op (mentat_silu_mul)."""
+    _require(gate.dtype in _GLUE_DTYPES and up.dtype == gate.dtype and up.shape == gate.shape,
+             "silu_mul takes bf16/f16 tensors of one shape")
+    _require(gate.is_contiguous() and up.is_contiguous(), "silu_mul takes contiguous tensors")
+    out = torch.empty_like(gate)
+    st = get_lib().mentat_silu_mul(ptr(gate), ptr(up), ptr(out), gate.numel(), DTYPE_CODES[gate.dtype],
+                                   stream_handle(gate.device))
+    check(st, "mentat_silu_mul")
+    return out
+
+
 def semantic_ema(vectors: list, hidden: torch.Tensor, fresh: list, alpha: float) -> None:
     """Fold row i of ``hidden`` [n, H] into ``vectors[i]`` (an H-element
     contiguous tensor on the same device, updated in place): copied when

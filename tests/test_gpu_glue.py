@@ -1,0 +1,101 @@
+"""Fused layer glue of the captured decode step against the modules it replaces:
+HF LlamaRMSNorm (with and without the residual add), the adapters'
+t*cos + rotate_half(t)*sin, and LlamaMLP's act_fn(gate) * up.
+
+RoPE is bit-exact (the same three roundings as torch's ops). RMSNorm and
+SiLU*up differ from torch only in the fp32 summation order of the mean and in
+exp's last bit. A one-ulp change of the fp32 scale can move the rounded
+normalised value by one unit, which the weight multiply (|w| up to ~2) can
+make two units of the output: RMSNorm is held to two units, SiLU*up to one,
+and both to differing from torch in under 1% of elements."""
+import pytest
+import torch
+
+from mentat_amd import ops
+from mentat_amd.adapters.model_adapter import rotate_half
+
+pytestmark = pytest.mark.gpu
+
+
+def _ulp(ref: torch.Tensor) -> torch.Tensor:
+    bits = 8 if ref.dtype == torch.bfloat16 else 11
+    mag = ref.float().abs().clamp_min(2.0 ** -14)
+    return torch.exp2(torch.floor(torch.log2(mag)) - (bits - 1))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("rows,H", [(1, 4096), (152, 4096), (7, 2048), (33, 5120), (3, 8)])
+def test_rmsnorm_matches_hf_module(gpu, dtype, rows, H):
+    from transformers.models.llama.modeling_llama import LlamaRMSNorm
+
+    print(f"case rmsnorm {dtype} rows={rows} H={H}", flush=True)
+    g = torch.Generator(device=gpu).manual_seed(rows * 7 + H)
+    norm = LlamaRMSNorm(H, eps=1e-5).to(gpu, dtype)
+    with torch.no_grad():
+        norm.weight.copy_((1 + 0.2 * torch.randn(H, generator=g, device=gpu)).to(dtype))
+    x = (3 * torch.randn(1, rows, H, generator=g, device=gpu)).to(dtype)
+    res = torch.randn(1, rows, H, generator=g, device=gpu).to(dtype)
+    with torch.no_grad():
+        for residual in (None, res):
+            h_ref = x if residual is None else residual + x
+            y_ref = norm(h_ref)
+            y, h = ops.rmsnorm(x, norm.weight, norm.variance_epsilon, residual=residual)
+            if residual is not None:
+                assert torch.equal(h, h_ref)  # the residual add rounds as torch's add
+            else:
+                assert h is None
+            diff = (y.float() - y_ref.float()).abs()
+            assert bool((diff <= 2 * _ulp(y_ref)).all()), float(diff.max())
+            assert (diff > 0).float().mean().item() < 0.01
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("n,Hq,Hk,D", [(152, 32, 8, 128), (5, 16, 2, 64), (1, 4, 4, 128)])
+def test_rope_bit_exact_with_rotate_half(gpu, dtype, n, Hq, Hk, D):
+    from transformers import LlamaConfig
+    from transformers.models.llama.modeling_llama import LlamaRotaryEmbedding
+
+    print(f"case rope {dtype} n={n} Hq={Hq} Hk={Hk} D={D}", flush=True)
+    g = torch.Generator(device=gpu).manual_seed(n + Hq + D)
+    cfg = LlamaConfig(hidden_size=Hq * D, num_attention_heads=Hq, num_key_value_heads=Hk, head_dim=D,
+                      max_position_embeddings=8192)
+    rot = LlamaRotaryEmbedding(cfg).to(gpu)
+    q = torch.randn(n, 1, Hq, D, generator=g, device=gpu).to(dtype)
+    k = torch.randn(n, 1, Hk, D, generator=g, device=gpu).to(dtype)
+    pos = torch.randint(0, 8000, (n, 1), generator=g, device=gpu)
+    cos, sin = rot(q, pos)
+    cos, sin = cos.unsqueeze(2), sin.unsqueeze(2)
+    q_ref = q * cos + rotate_half(q) * sin
+    k_ref = k * cos + rotate_half(k) * sin
+    ops.rope_(q, k, cos, sin)
+    assert torch.equal(q, q_ref)
+    assert torch.equal(k, k_ref)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("rows,F", [(152, 14336), (1, 8), (9, 1024)])
+def test_silu_mul_matches_mlp_activation(gpu, dtype, rows, F):
+    print(f"case silu_mul {dtype} rows={rows} F={F}", flush=True)
+    g = torch.Generator(device=gpu).manual_seed(rows + F)
+    gate = (4 * torch.randn(1, rows, F, generator=g, device=gpu)).to(dtype)
+    up = torch.randn(1, rows, F, generator=g, device=gpu).to(dtype)
+    ref = torch.nn.functional.silu(gate) * up
+    out = ops.silu_mul(gate, up)
+    diff = (out.float() - ref.float()).abs()
+    assert bool((diff <= _ulp(ref)).all()), float(diff.max())
+    assert (diff > 0).float().mean().item() < 0.01
+
+
+def test_captured_step_fuses_the_glue(gpu):
+    """A bf16 HF Llama model takes the fused captured path; an fp32 one does not."""
+    from transformers import LlamaConfig, LlamaForCausalLM
+
+    from mentat_amd.adapters.adapter_factory import get_adapter
+    from mentat_amd.core.graph_decode import _fusable
+
+    cfg = LlamaConfig(hidden_size=256, num_hidden_layers=2, num_attention_heads=4, num_key_value_heads=2,
+                      head_dim=64, intermediate_size=512, vocab_size=1000)
+    model = LlamaForCausalLM(cfg).to(gpu)
+    assert not _fusable(get_adapter(model), torch.float32)
+    model = model.to(torch.bfloat16)
+    assert _fusable(get_adapter(model), torch.bfloat16)
