@@ -204,9 +204,16 @@ int mentat_semantic_similar(const int64_t* ptrs, const int32_t* parent_key, cons
  * mentat_rope: in place on q [rows][Hq][D] and k [rows][Hk][D] with cos/sin
  * [rows][D]: t = rnd(rnd(t * cos) + rnd(rotate_half(t) * sin)).
  *
- * mentat_silu_mul: out = rnd(rnd(silu(gate)) * up) over n elements
- * (n % 8 == 0, 16-byte aligned), silu(g) = g / (1 + exp(-g)) in fp32
- * (the LlamaMLP / Qwen3MLP activation and product).
+ * mentat_rope_qkv: the same rotation, reading row r's q, k and v heads from one
+ * merged projection output (qkv + r * row_stride: Hq q heads, then Hk k heads,
+ * then Hk v heads) and writing rotated q, rotated k and plain v to dense
+ * [rows][H][D] buffers (q_proj / k_proj / v_proj computed as one GEMM).
+ *
+ * mentat_silu_mul: out[r][j] = rnd(rnd(silu(gate[r][j])) * up[r][j]) for
+ * j < F (F % 8 == 0), gate and up rows in_row_stride elements apart (F for
+ * separate tensors, 2F for the halves of a merged gate/up projection), out
+ * dense [rows][F], 16-byte aligned; silu(g) = g / (1 + exp(-g)) in fp32 (the
+ * LlamaMLP / Qwen3MLP activation and product).
  * ------------------------------------------------------------------------ */
 int mentat_rmsnorm(const void* x, const void* residual_in, void* residual_out, const void* weight, void* out,
                    int rows, int H, float eps, int dtype, void* stream);
@@ -214,7 +221,11 @@ int mentat_rmsnorm(const void* x, const void* residual_in, void* residual_out, c
 int mentat_rope(void* q, void* k, const void* cos, const void* sin, int rows, int Hq, int Hk, int D, int dtype,
                 void* stream);
 
-int mentat_silu_mul(const void* gate, const void* up, void* out, int64_t n, int dtype, void* stream);
+int mentat_rope_qkv(const void* qkv, int64_t row_stride, void* q, void* k, void* v, const void* cos,
+                    const void* sin, int rows, int Hq, int Hk, int D, int dtype, void* stream);
+
+int mentat_silu_mul(const void* gate, const void* up, void* out, int rows, int F, int64_t in_row_stride, int dtype,
+                    void* stream);
 
 /* ------------------------------------------------------------------------
  * KV append: write n new token rows into the pools, fused with the lazy

@@ -85,7 +85,14 @@ SIGNATURES: dict[str, tuple] = {
             _c_int, _c_int, _c_int, _c_int, _c_int, _c_void_p,  # rows, Hq, Hk, D, dtype, stream
         ],
     ),
-    "mentat_silu_mul": (_c_int, [_c_void_p, _c_void_p, _c_void_p, _c_i64, _c_int, _c_void_p]),
+    "mentat_rope_qkv": (
+        _c_int,
+        [
+            _c_void_p, _c_i64, _c_void_p, _c_void_p, _c_void_p,  # qkv, row_stride, q, k, v
+            _c_void_p, _c_void_p, _c_int, _c_int, _c_int, _c_int, _c_int, _c_void_p,  # cos, sin, rows, Hq, Hk, D, dtype, stream
+        ],
+    ),
+    "mentat_silu_mul": (_c_int, [_c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, _c_i64, _c_int, _c_void_p]),
     "mentat_semantic_ema": (
         _c_int,
         [

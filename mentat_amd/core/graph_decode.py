@@ -32,7 +32,11 @@ For 16-bit HF Llama/Qwen3-style models whose adapter keeps the stock glue, the
 captured layer also fuses that glue: each residual add with the RMSNorm that
 follows it (across the layer boundary too), RoPE of Q and K in one launch, and
 SiLU(gate) * up (ops.rmsnorm, ops.rope_, ops.silu_mul); other models run their
-modules as they are.
+modules as they are. Without QK-norm (Llama) the q/k/v projections also run
+as one GEMM and gate/up as another: each layer's weights are concatenated once
+and the modules' own weights become views into the merged tensors (no second
+copy; the eager path reads the same storage). If a module's weight is later
+rebound (e.g. ``model.to``), the next step merges again and recaptures.
 
 No object is destroyed while a capture is active: the garbage collector runs
 just before each capture and stays disabled during it. (A finished run's
@@ -62,6 +66,10 @@ __all__ = ["DecodeGraphs", "BUCKETS"]
 # 7.2 ms for 160, 6.1 ms for 184 but 8.2 ms for 192. The buckets skip those
 # row counts and step by 16 where the cost rises with the rows.
 BUCKETS = (8, 16, 32, 48, 64, 80, 88, 104, 120, 136, 152, 168, 184, 200, 216, 232, 248, 256)
+# With q/k/v and gate/up merged the GEMM costs move again (the merged q/k/v GEMM
+# is slow at 128-160 rows: the 32 layers' projections take 5.5-6.1 ms there but
+# 5.2 ms at 176): the buckets that no larger one undercuts.
+MERGED_BUCKETS = (8, 16, 24, 32, 40, 56, 64, 72, 80, 88, 112, 120, 176, 184, 200, 208, 216, 232, 240, 248, 256)
 
 
 def _fusable(a, dtype) -> bool:
@@ -89,6 +97,33 @@ def _fusable(a, dtype) -> bool:
     return norm_ok(a.final_norm)
 
 
+def _mergeable(a) -> bool:
+    """Q/K/V and gate/up may run as one GEMM each: Llama projections (no
+    QK-norm), bias-free linear layers."""
+    from ..adapters.llama_adapter import LlamaAdapter
+
+    if type(a).project_qkv is not LlamaAdapter.project_qkv:
+        return False
+    for block in a.layers:
+        attn, mlp = block.self_attn, block.mlp
+        for lin in (attn.q_proj, attn.k_proj, attn.v_proj, mlp.gate_proj, mlp.up_proj):
+            if not isinstance(lin, torch.nn.Linear) or lin.bias is not None:
+                return False
+    return True
+
+
+def _merge_linears(lins) -> torch.Tensor:
+    """One weight [sum(out), in] for the bias-free linears ``lins``; each
+    module's weight becomes a view of its rows."""
+    w = torch.cat([lin.weight.detach() for lin in lins], dim=0)
+    off = 0
+    for lin in lins:
+        n = lin.weight.shape[0]
+        lin.weight.data = w[off:off + n]
+        off += n
+    return w
+
+
 class _Bucket:
     __slots__ = ("n", "graph", "dev", "host", "host_np", "logits", "hidden", "version")
 
@@ -96,17 +131,40 @@ class _Bucket:
 class DecodeGraphs:
     """Captured batched decode forwards for one PagedModelWrapper."""
 
-    def __init__(self, wrapper, buckets=BUCKETS):
+    def __init__(self, wrapper, buckets=None):
         self.a = wrapper.adapter
         self.m = wrapper.kv_cache_mgr
         self.dev = wrapper.device
-        self.buckets = tuple(sorted(buckets))
-        self.max_batch = self.buckets[-1]
         self._graphs: dict[int, _Bucket] = {}
         self._stream = torch.cuda.Stream(self.dev)
         self._ws = None
         self.captures = 0
         self.fused = _fusable(self.a, self.m.dtype)
+        self.merged = self.fused and _mergeable(self.a)
+        self._w_qkv: list = []
+        self._w_gu: list = []
+        if self.merged:
+            self._merge()
+        if buckets is None:
+            buckets = MERGED_BUCKETS if self.merged else BUCKETS
+        self.buckets = tuple(sorted(buckets))
+        self.max_batch = self.buckets[-1]
+
+    def _merge(self) -> None:
+        with torch.no_grad():
+            self._w_qkv = [_merge_linears((b.self_attn.q_proj, b.self_attn.k_proj, b.self_attn.v_proj))
+                           for b in self.a.layers]
+            self._w_gu = [_merge_linears((b.mlp.gate_proj, b.mlp.up_proj)) for b in self.a.layers]
+
+    def _merged_current(self) -> bool:
+        """The modules' weights still view the merged tensors (first and last layer)."""
+        layers = self.a.layers
+        for i in (0, len(layers) - 1):
+            b = layers[i]
+            if (b.self_attn.q_proj.weight.data_ptr() != self._w_qkv[i].data_ptr()
+                    or b.mlp.gate_proj.weight.data_ptr() != self._w_gu[i].data_ptr()):
+                return False
+        return True
 
     # ------------------------------------------------------------------
     def bucket(self, n: int):
@@ -186,23 +244,34 @@ class DecodeGraphs:
         hidden = a.embeddings(ids)                     # [1, nb, H]: the residual stream
         ln = layers[0].input_layernorm
         x, _ = ops.rmsnorm(hidden, ln.weight, ln.variance_epsilon)
+        Hq, Hk = a.num_attention_heads, a.num_key_value_heads
         for layer_idx, block in enumerate(layers):
             attn = a.get_self_attn(block)
-            q, k, v = a.project_qkv(attn, x.squeeze(0).unsqueeze(1))  # one token per sequence
-            cos, sin = a._build_cos_sin(pos, q)
-            q, k = q.contiguous(), k.contiguous()
-            ops.rope_(q, k, cos, sin)
-            ops.kv_append(k.squeeze(1).to(m.dtype).contiguous(), v.squeeze(1).to(m.dtype).contiguous(),
+            if self.merged:
+                qkv = torch.nn.functional.linear(x, self._w_qkv[layer_idx])  # [1, nb, (Hq + 2 Hk) * D]
+                cos, sin = a._build_cos_sin(pos, qkv)
+                q, k, v = ops.rope_qkv(qkv, Hq, Hk, cos, sin)               # dense [nb, H, D]
+            else:
+                q, k, v = a.project_qkv(attn, x.squeeze(0).unsqueeze(1))  # one token per sequence
+                cos, sin = a._build_cos_sin(pos, q)
+                q, k = q.contiguous(), k.contiguous()
+                ops.rope_(q, k, cos, sin)
+                q, k, v = q.squeeze(1), k.squeeze(1), v.squeeze(1)
+            ops.kv_append(k.to(m.dtype).contiguous(), v.to(m.dtype).contiguous(),
                           m._k_store, m._v_store, plans[layer_idx], block_size=m.block_size, layout=m.layout,
                           block_tables=m._tables[layer_idx], seq_lens=m._lens[layer_idx])
-            o = ops.paged_decode(q.squeeze(1), m._k_store, m._v_store, layout=m.layout,
+            o = ops.paged_decode(q, m._k_store, m._v_store, layout=m.layout,
                                  block_tables=m._tables[layer_idx], seq_lens=m._lens[layer_idx], seq_rows=rows,
                                  max_seqlen=max_seqlen)
             attn_out = attn.o_proj(o.reshape(1, nb, -1))
             ln = block.post_attention_layernorm
             x, hidden = ops.rmsnorm(attn_out, ln.weight, ln.variance_epsilon, residual=hidden)
             mlp = block.mlp
-            mlp_out = mlp.down_proj(ops.silu_mul(mlp.gate_proj(x), mlp.up_proj(x)))
+            if self.merged:
+                act = ops.silu_mul_merged(torch.nn.functional.linear(x, self._w_gu[layer_idx]))
+            else:
+                act = ops.silu_mul(mlp.gate_proj(x), mlp.up_proj(x))
+            mlp_out = mlp.down_proj(act)
             ln = layers[layer_idx + 1].input_layernorm if layer_idx + 1 < L else a.final_norm
             x, hidden = ops.rmsnorm(mlp_out, ln.weight, ln.variance_epsilon, residual=hidden)
         x = x.squeeze(0)
@@ -266,6 +335,9 @@ class DecodeGraphs:
         nb = self.bucket(n)
         if nb is None:
             return None
+        if self.merged and not self._merged_current():
+            self._merge()           # weights were rebound: merge again, capture again
+            self._graphs.clear()
         m = self.m
         offsets = [m.get_kv_length(s) for s in seq_ids]  # RoPE positions: lengths before the append
         rows = [m._sequences[s].row for s in seq_ids]

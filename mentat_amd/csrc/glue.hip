@@ -110,36 +110,61 @@ __global__ __launch_bounds__(kNormThreads) void rmsnorm_kernel(const uint16_t* x
   }
 }
 
-// Rotary embedding in place on q [rows][Hq][D] and k [rows][Hk][D] with
-// cos/sin [rows][D]: one thread per (row, head, i < D/2) rotates the pair
-// (i, i + D/2). Grid: rows x ceil((Hq + Hk) * D/2 / 256).
+// Rotary embedding of q (Hq heads) and k (Hk heads) with cos/sin [rows][D]: head h of
+// row r is read at qi/ki + r * in_stride + h * D and written at qo/ko + (r * H + h) * D
+// (in place when the pointers agree and in_stride = H * D); with vi/vo, the row's Hk v
+// heads are copied the same way. One thread per (row, head, i < D/2) rotates the pair
+// (i, i + D/2). Grid: rows x ceil((Hq + 2 Hk) * D/2 / 256).
 template <typename T>
-__global__ __launch_bounds__(256) void rope_kernel(uint16_t* q, uint16_t* k, const uint16_t* cs, const uint16_t* sn,
-                                                   int Hq, int Hk, int D) {
+__global__ __launch_bounds__(256) void rope_kernel(const uint16_t* qi, uint16_t* qo, const uint16_t* ki, uint16_t* ko,
+                                                   const uint16_t* vi, uint16_t* vo, long q_stride, long k_stride,
+                                                   long v_stride, const uint16_t* cs, const uint16_t* sn, int Hq,
+                                                   int Hk, int D) {
   using E = G16<T>;
   const int row = blockIdx.x;
   const int half = D / 2;
   const int idx = blockIdx.y * 256 + threadIdx.x;
-  if (idx >= (Hq + Hk) * half) return;
+  const int nv = vi ? Hk : 0;
+  if (idx >= (Hq + Hk + nv) * half) return;
   const int hd = idx / half, i = idx - hd * half;
-  uint16_t* t = hd < Hq ? q + ((long)row * Hq + hd) * D : k + ((long)row * Hk + (hd - Hq)) * D;
+  if (hd >= Hq + Hk) {  // v: copied
+    const int h = hd - Hq - Hk;
+    const uint16_t* src = vi + (long)row * v_stride + (long)h * D;
+    uint16_t* dst = vo + ((long)row * Hk + h) * D;
+    dst[i] = src[i];
+    dst[i + half] = src[i + half];
+    return;
+  }
+  const uint16_t* src;
+  uint16_t* dst;
+  if (hd < Hq) {
+    src = qi + (long)row * q_stride + (long)hd * D;
+    dst = qo + ((long)row * Hq + hd) * D;
+  } else {
+    src = ki + (long)row * k_stride + (long)(hd - Hq) * D;
+    dst = ko + ((long)row * Hk + (hd - Hq)) * D;
+  }
   auto ld = [](const uint16_t* p, int j) { return E::lo((uint32_t)p[j]); };
   const uint16_t* c = cs + (long)row * D;
   const uint16_t* s = sn + (long)row * D;
-  const float a = ld(t, i), b = ld(t, i + half);
+  const float a = ld(src, i), b = ld(src, i + half);
   const float ya = E::rnd(E::rnd(a * ld(c, i)) + E::rnd(-b * ld(s, i)));
   const float yb = E::rnd(E::rnd(b * ld(c, i + half)) + E::rnd(a * ld(s, i + half)));
-  t[i] = (uint16_t)E::bits(ya);
-  t[i + half] = (uint16_t)E::bits(yb);
+  dst[i] = (uint16_t)E::bits(ya);
+  dst[i + half] = (uint16_t)E::bits(yb);
 }
 
-// m = rnd(rnd(silu(g)) * u) over n elements (n % 8 == 0), 8 per thread.
+// m[r][j] = rnd(rnd(silu(g[r][j])) * u[r][j]) for rows r and j < F (F % 8 == 0): g and u rows
+// in_stride elements apart, m dense; 8 elements per thread, grid ceil(rows * F / 8 / 256).
 template <typename T>
-__global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t* g, const uint16_t* u, uint16_t* m, long n8) {
+__global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t* g, const uint16_t* u, uint16_t* m, long n8,
+                                                       int F8, long in_stride) {
   using E = G16<T>;
   const long i = (long)blockIdx.x * 256 + threadIdx.x;
   if (i >= n8) return;
-  const uint4 gv = *(const uint4*)(g + 8 * i), uv = *(const uint4*)(u + 8 * i);
+  const long r = i / F8, c = i - r * F8;
+  const long io = r * in_stride + 8 * c;
+  const uint4 gv = *(const uint4*)(g + io), uv = *(const uint4*)(u + io);
   const uint32_t gs[4] = {gv.x, gv.y, gv.z, gv.w}, us[4] = {uv.x, uv.y, uv.z, uv.w};
   uint32_t o[4];
 #pragma unroll
@@ -188,41 +213,69 @@ extern "C" int mentat_rmsnorm(const void* x, const void* residual_in, void* resi
   return (int)hipGetLastError();
 }
 
+static int rope_launch(const void* qi, void* qo, const void* ki, void* ko, const void* vi, void* vo, int64_t qs,
+                       int64_t ks, int64_t vs, const void* cos, const void* sin, int rows, int Hq, int Hk, int D,
+                       int dtype, void* stream) {
+  const int nh = Hq + Hk + (vi ? Hk : 0);
+  const dim3 grid(rows, (nh * (D / 2) + 255) / 256);
+  hipStream_t s = (hipStream_t)stream;
+  const auto* c = (const uint16_t*)cos;
+  const auto* sn = (const uint16_t*)sin;
+  switch (dtype) {
+    case MENTAT_BF16:
+      hipLaunchKernelGGL(rope_kernel<BF16>, grid, dim3(256), 0, s, (const uint16_t*)qi, (uint16_t*)qo,
+                         (const uint16_t*)ki, (uint16_t*)ko, (const uint16_t*)vi, (uint16_t*)vo, (long)qs, (long)ks,
+                         (long)vs, c, sn, Hq, Hk, D);
+      break;
+    case MENTAT_F16:
+      hipLaunchKernelGGL(rope_kernel<F16>, grid, dim3(256), 0, s, (const uint16_t*)qi, (uint16_t*)qo,
+                         (const uint16_t*)ki, (uint16_t*)ko, (const uint16_t*)vi, (uint16_t*)vo, (long)qs, (long)ks,
+                         (long)vs, c, sn, Hq, Hk, D);
+      break;
+    default:
+      return MENTAT_EUNSUP;
+  }
+  return (int)hipGetLastError();
+}
+
 extern "C" int mentat_rope(void* q, void* k, const void* cos, const void* sin, int rows, int Hq, int Hk, int D,
                            int dtype, void* stream) {
   if (rows < 0 || Hq < 0 || Hk < 0 || D <= 0 || D % 2 != 0) return MENTAT_EINVAL;
   if (rows == 0 || Hq + Hk == 0) return MENTAT_OK;
   if ((Hq && !q) || (Hk && !k) || !cos || !sin) return MENTAT_EINVAL;
-  hipStream_t s = (hipStream_t)stream;
-  const dim3 grid(rows, ((Hq + Hk) * (D / 2) + 255) / 256);
-  auto* qo = (uint16_t*)q;
-  auto* ko = (uint16_t*)k;
-  const auto* c = (const uint16_t*)cos;
-  const auto* sn = (const uint16_t*)sin;
-  switch (dtype) {
-    case MENTAT_BF16: hipLaunchKernelGGL(rope_kernel<BF16>, grid, dim3(256), 0, s, qo, ko, c, sn, Hq, Hk, D); break;
-    case MENTAT_F16: hipLaunchKernelGGL(rope_kernel<F16>, grid, dim3(256), 0, s, qo, ko, c, sn, Hq, Hk, D); break;
-    default: return MENTAT_EUNSUP;
-  }
-  return (int)hipGetLastError();
+  return rope_launch(q, q, k, k, nullptr, nullptr, (int64_t)Hq * D, (int64_t)Hk * D, 0, cos, sin, rows, Hq, Hk, D,
+                     dtype, stream);
 }
 
-extern "C" int mentat_silu_mul(const void* gate, const void* up, void* out, int64_t n, int dtype, void* stream) {
-  if (n < 0) return MENTAT_EINVAL;
-  if (n == 0) return MENTAT_OK;
+extern "C" int mentat_rope_qkv(const void* qkv, int64_t row_stride, void* q, void* k, void* v, const void* cos,
+                               const void* sin, int rows, int Hq, int Hk, int D, int dtype, void* stream) {
+  if (rows < 0 || Hq <= 0 || Hk <= 0 || D <= 0 || D % 2 != 0 || row_stride < (int64_t)(Hq + 2 * Hk) * D)
+    return MENTAT_EINVAL;
+  if (rows == 0) return MENTAT_OK;
+  if (!qkv || !q || !k || !v || !cos || !sin) return MENTAT_EINVAL;
+  const auto* b = (const uint16_t*)qkv;
+  return rope_launch(b, q, b + (long)Hq * D, k, b + (long)(Hq + Hk) * D, v, row_stride, row_stride, row_stride, cos,
+                     sin, rows, Hq, Hk, D, dtype, stream);
+}
+
+extern "C" int mentat_silu_mul(const void* gate, const void* up, void* out, int rows, int F, int64_t in_row_stride,
+                               int dtype, void* stream) {
+  if (rows < 0 || F < 0 || in_row_stride < F) return MENTAT_EINVAL;
+  if (rows == 0 || F == 0) return MENTAT_OK;
   if (!gate || !up || !out) return MENTAT_EINVAL;
-  if (n % 8 != 0 || !aligned16(gate) || !aligned16(up) || !aligned16(out)) return MENTAT_EUNSUP;
+  if (F % 8 != 0 || in_row_stride % 8 != 0 || !aligned16(gate) || !aligned16(up) || !aligned16(out))
+    return MENTAT_EUNSUP;
   hipStream_t s = (hipStream_t)stream;
-  const long n8 = n / 8;
+  const long n8 = (long)rows * (F / 8);
   const dim3 grid((unsigned)((n8 + 255) / 256));
   switch (dtype) {
     case MENTAT_BF16:
       hipLaunchKernelGGL(silu_mul_kernel<BF16>, grid, dim3(256), 0, s, (const uint16_t*)gate, (const uint16_t*)up,
-                         (uint16_t*)out, n8);
+                         (uint16_t*)out, n8, F / 8, (long)in_row_stride);
       break;
     case MENTAT_F16:
       hipLaunchKernelGGL(silu_mul_kernel<F16>, grid, dim3(256), 0, s, (const uint16_t*)gate, (const uint16_t*)up,
-                         (uint16_t*)out, n8);
+                         (uint16_t*)out, n8, F / 8, (long)in_row_stride);
       break;
     default:
       return MENTAT_EUNSUP;

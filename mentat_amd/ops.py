@@ -268,14 +268,50 @@ def rope_(q: torch.Tensor, k: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor
     check(st, "mentat_rope")
 
 
+def rope_qkv(qkv: torch.Tensor, Hq: int, Hk: int, cos: torch.Tensor, sin: torch.Tensor):
+    """Split a merged q/k/v projection output (rows of Hq + 2 Hk heads of D,
+    last dim dense) into dense q [rows, Hq, D], k and v [rows, Hk, D], with
+    RoPE applied to q and k (mentat_rope_qkv)."""
+    _require(qkv.dtype in _GLUE_DTYPES and cos.dtype == qkv.dtype and sin.dtype == qkv.dtype,
+             "rope_qkv takes bf16/f16 tensors of one dtype")
+    _require(qkv.stride(-1) == 1 and cos.is_contiguous() and sin.is_contiguous(), "dense rows required")
+    D = cos.shape[-1]
+    rows = cos.numel() // D
+    W = (Hq + 2 * Hk) * D
+    _require(qkv.shape[-1] == W and qkv.numel() == rows * W and qkv.is_contiguous(),
+             "qkv must be contiguous [rows, (Hq + 2 Hk) * D]")
+    q = torch.empty(rows, Hq, D, dtype=qkv.dtype, device=qkv.device)
+    k = torch.empty(rows, Hk, D, dtype=qkv.dtype, device=qkv.device)
+    v = torch.empty(rows, Hk, D, dtype=qkv.dtype, device=qkv.device)
+    st = get_lib().mentat_rope_qkv(ptr(qkv), W, ptr(q), ptr(k), ptr(v), ptr(cos), ptr(sin), rows, Hq, Hk, D,
+                                   DTYPE_CODES[qkv.dtype], stream_handle(qkv.device))
+    check(st, "mentat_rope_qkv")
+    return q, k, v
+
+
 def silu_mul(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
     """silu(gate) * up with torch's rounding per op (mentat_silu_mul)."""
     _require(gate.dtype in _GLUE_DTYPES and up.dtype == gate.dtype and up.shape == gate.shape,
              "silu_mul takes bf16/f16 tensors of one shape")
     _require(gate.is_contiguous() and up.is_contiguous(), "silu_mul takes contiguous tensors")
     out = torch.empty_like(gate)
-    st = get_lib().mentat_silu_mul(ptr(gate), ptr(up), ptr(out), gate.numel(), DTYPE_CODES[gate.dtype],
+    F = gate.shape[-1]
+    st = get_lib().mentat_silu_mul(ptr(gate), ptr(up), ptr(out), gate.numel() // F, F, F, DTYPE_CODES[gate.dtype],
                                    stream_handle(gate.device))
+    check(st, "mentat_silu_mul")
+    return out
+
+
+def silu_mul_merged(gu: torch.Tensor) -> torch.Tensor:
+    """silu(gate) * up from a merged gate/up projection output [..., 2F]
+    (gate = first half of each row, up = second half): [..., F]."""
+    _require(gu.dtype in _GLUE_DTYPES and gu.is_contiguous() and gu.shape[-1] % 2 == 0,
+             "silu_mul_merged takes a contiguous bf16/f16 [..., 2F] tensor")
+    F = gu.shape[-1] // 2
+    rows = gu.numel() // (2 * F)
+    out = torch.empty(*gu.shape[:-1], F, dtype=gu.dtype, device=gu.device)
+    st = get_lib().mentat_silu_mul(ptr(gu), gu.data_ptr() + F * gu.element_size(), ptr(out), rows, F, 2 * F,
+                                   DTYPE_CODES[gu.dtype], stream_handle(gu.device))
     check(st, "mentat_silu_mul")
     return out
 

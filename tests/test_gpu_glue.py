@@ -86,6 +86,38 @@ def test_silu_mul_matches_mlp_activation(gpu, dtype, rows, F):
     assert (diff > 0).float().mean().item() < 0.01
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_rope_qkv_splits_a_merged_projection(gpu, dtype):
+    """q/k/v read from one merged projection output: q and k rotated exactly as
+    rotate_half does on the split tensors, v copied."""
+    from transformers import LlamaConfig
+    from transformers.models.llama.modeling_llama import LlamaRotaryEmbedding
+
+    n, Hq, Hk, D = 37, 32, 8, 128
+    print(f"case rope_qkv {dtype} n={n}", flush=True)
+    g = torch.Generator(device=gpu).manual_seed(5)
+    cfg = LlamaConfig(hidden_size=Hq * D, num_attention_heads=Hq, num_key_value_heads=Hk, head_dim=D)
+    rot = LlamaRotaryEmbedding(cfg).to(gpu)
+    qkv = torch.randn(1, n, (Hq + 2 * Hk) * D, generator=g, device=gpu).to(dtype)
+    pos = torch.randint(0, 4000, (n, 1), generator=g, device=gpu)
+    cos, sin = rot(qkv, pos)
+    cos, sin = cos.unsqueeze(2), sin.unsqueeze(2)
+    q, k, v = ops.rope_qkv(qkv, Hq, Hk, cos, sin)
+    x = qkv.view(n, 1, Hq + 2 * Hk, D)
+    q0, k0, v0 = x[:, :, :Hq], x[:, :, Hq:Hq + Hk], x[:, :, Hq + Hk:]
+    assert torch.equal(q, (q0 * cos + rotate_half(q0) * sin).squeeze(1))
+    assert torch.equal(k, (k0 * cos + rotate_half(k0) * sin).squeeze(1))
+    assert torch.equal(v, v0.squeeze(1))
+
+
+def test_silu_mul_merged_matches_split_halves(gpu):
+    g = torch.Generator(device=gpu).manual_seed(6)
+    gu = (3 * torch.randn(1, 41, 2 * 14336, generator=g, device=gpu)).to(torch.bfloat16)
+    out = ops.silu_mul_merged(gu)
+    ref = ops.silu_mul(gu[..., :14336].contiguous(), gu[..., 14336:].contiguous())
+    assert torch.equal(out, ref)
+
+
 def test_captured_step_fuses_the_glue(gpu):
     """A bf16 HF Llama model takes the fused captured path; an fp32 one does not."""
     from transformers import LlamaConfig, LlamaForCausalLM
@@ -99,3 +131,6 @@ def test_captured_step_fuses_the_glue(gpu):
     assert not _fusable(get_adapter(model), torch.float32)
     model = model.to(torch.bfloat16)
     assert _fusable(get_adapter(model), torch.bfloat16)
+    from mentat_amd.core.graph_decode import _mergeable
+
+    assert _mergeable(get_adapter(model))

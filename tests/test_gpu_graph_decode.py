@@ -178,3 +178,29 @@ def test_no_garbage_collection_during_capture(gpu):
     assert any(c for c, _ in seen) and any(not c for c, _ in seen)
     assert all(not on for capturing, on in seen if capturing)
     assert gc.isenabled()
+
+
+def test_rebound_weights_are_merged_again(gpu):
+    """The captured Llama step runs q/k/v and gate/up as merged GEMMs over views of
+    the modules' weights; rebinding a weight (a new tensor) is detected on the next
+    step, which merges again and recaptures, so its logits follow the new weights."""
+    print("case merged projections after a weight rebind", flush=True)
+    model = _bf16_model()
+    we, wg = _wrapper(model, False), _wrapper(model, True)
+    with torch.no_grad():
+        ids = torch.tensor([[3, 1, 4, 1, 5, 9, 2, 6]], device="cuda")
+        se, sg = we.kv_cache_mgr.allocate_sequence(), wg.kv_cache_mgr.allocate_sequence()
+        we.prefill(ids, se)
+        wg.prefill(ids, sg)
+        le, _ = we.decode_batch_tensor([7], [se])
+        lg, _ = wg.decode_batch_tensor([7], [sg])
+        assert wg.graphs.merged
+        assert float((lg.float() - le.float()).abs().max()) <= 2e-2 * float(le.float().abs().max()) + 2e-2
+        n0 = wg.graphs.captures
+        for b in model.model.layers:  # new tensors, new values
+            b.self_attn.q_proj.weight.data = (b.self_attn.q_proj.weight.data * 1.5).clone()
+            b.mlp.gate_proj.weight.data = (b.mlp.gate_proj.weight.data * 0.5).clone()
+        le, _ = we.decode_batch_tensor([8], [se])
+        lg, _ = wg.decode_batch_tensor([8], [sg])
+        assert wg.graphs.captures > n0
+        assert float((lg.float() - le.float()).abs().max()) <= 2e-2 * float(le.float().abs().max()) + 2e-2
