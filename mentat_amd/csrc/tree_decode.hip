@@ -86,7 +86,8 @@ struct TreeParams {
 constexpr int kTreeWaves = 8;
 constexpr int kTreeThreads = 64 * kTreeWaves;
 constexpr int kTreePrefetch = 4;        // shared path: tiles in flight per loading thread (even)
-constexpr int kTreeSharedMaxTiles = 16;  // shared path: tiles per task (host-enforced)
+constexpr int kTreeSharedMaxTiles = 32;  // shared path: tiles per task (host-enforced)
+static_assert(kTreeSharedMaxTiles <= 64, "the task's tile mask is 64 bits");
 constexpr float kTreeSlack = 8.f;
 
 typedef const int32_t __attribute__((address_space(4)))* tconst_i32;
@@ -270,7 +271,7 @@ __device__ __forceinline__ void tree_shared(const TreeParams& p, const int32_t* 
   // Block ids of the task's tiles, read once into scalar registers (tiles
   // past the chunk repeat the last one and are masked).
   int blk[kTreeSharedMaxTiles];
-  unsigned okm = 0;  // bit i: tile i is inside the chunk and its page id is in range
+  uint64_t okm = 0;  // bit i: tile i is inside the chunk and its page id is in range
   static_for<kTreeSharedMaxTiles>([&](auto ic) __attribute__((always_inline)) {
     constexpr int i = decltype(ic)::value;
     const int tt = t_first + (i < ntile ? i : ntile - 1);
@@ -278,7 +279,7 @@ __device__ __forceinline__ void tree_shared(const TreeParams& p, const int32_t* 
     const int b = tld(trow, pg);
     const bool ok = i < ntile && b >= 0 && b < p.num_blocks;
     blk[i] = ok ? b : 0;
-    okm |= ok ? (1u << i) : 0u;
+    okm |= ok ? (1ull << i) : 0ull;
   });
 
   // This thread's 16-byte piece of every tile: waves [0, 2D/64) carry K,
@@ -302,7 +303,7 @@ __device__ __forceinline__ void tree_shared(const TreeParams& p, const int32_t* 
     constexpr int i = decltype(ic)::value;
     const int t = t_first + i;
     const int sub = t - (t / NSUB) * NSUB;
-    const bool ok = loader && ((okm >> i) & 1u);
+    const bool ok = loader && ((okm >> i) & 1ull);
     const long ph = ((long)blk[i] * p.Hkv + head) * (long)(B * D);
     const __amdgpu_buffer_rsrc_t r = trsrc(base + ph, ok ? B * D * (int)sizeof(S) : 0);
     const int soff = (is_k ? sub * 16 * D : sub * 16) * (int)sizeof(S);
@@ -365,7 +366,7 @@ __device__ __forceinline__ void tree_shared(const TreeParams& p, const int32_t* 
           const uint2 a1 = *(const uint2*)__builtin_assume_aligned(stg + L::STAGE + vo, 8);
           vb[j] = make_uint4(a0.x, a0.y, a1.x, a1.y);
         }
-        w.tile2(p, t_first + i0, (okm >> i0) & 1u, (okm >> (i0 + 1)) & 1u, valid, k0, k1, vb);
+        w.tile2(p, t_first + i0, (okm >> i0) & 1ull, (okm >> (i0 + 1)) & 1ull, valid, k0, k1, vb);
       }
     }
   });

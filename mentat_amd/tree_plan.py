@@ -26,7 +26,7 @@ import numpy as np
 
 ITEM_FIELDS = 8
 WAVES_PER_WG = 8
-SHARED_MAX_TILES = 16  # tiles per shared task (the kernel's unrolled tile loop)
+SHARED_MAX_TILES = 32  # tiles per shared task (the kernel's unrolled tile loop)
 
 
 @dataclass
@@ -152,7 +152,7 @@ def find_segments(tables: list, lens: list, rows: list, block_size: int) -> list
 
 
 def build_plan(tables: list, lens: list, rows: list, *, block_size: int, Hkv: int, G: int,
-               chunk_tiles: int = 4, shared_chunk_tiles: int = 16, shared_min_groups: int = 3) -> TreePlan:
+               chunk_tiles: int = 4, shared_chunk_tiles: int = 32, shared_min_groups: int = 3) -> TreePlan:
     """Segments -> shared tasks, solo items and per-(query, head) partial slots."""
     if G < 1 or 16 % G:
         raise ValueError("query heads per kv head must divide 16")

@@ -13,7 +13,7 @@ import torch
 
 from mentat_amd import ops
 from mentat_amd._lib import LAYOUT_NATIVE
-from mentat_amd.tree_plan import build_plan
+from mentat_amd.tree_plan import SHARED_MAX_TILES, build_plan
 from mentat_amd.workloads import logical_views, prefix_tree_batch
 from oracle.attention import paged_decode_f64
 
@@ -35,10 +35,14 @@ def _oracle(tb, idx=None):
     return paged_decode_f64(q, kc, vc, tabs, [tb.lens[i] for i in idx], tb.block_size, tb.scale)
 
 
-def _run_tree(tb, chunk_tiles=16, min_groups=3):
+def _run_tree(tb, chunk_tiles=16, min_groups=3, defaults=False):
     G = tb.q.shape[1] // tb.k_store.shape[1]
-    plan = build_plan(tb.tables, tb.lens, tb.rows, block_size=tb.block_size, Hkv=tb.k_store.shape[1], G=G,
-                      chunk_tiles=chunk_tiles, shared_chunk_tiles=min(16, chunk_tiles + 1), shared_min_groups=min_groups)
+    if defaults:  # the plan the bench and the generator use
+        plan = build_plan(tb.tables, tb.lens, tb.rows, block_size=tb.block_size, Hkv=tb.k_store.shape[1], G=G)
+    else:
+        plan = build_plan(tb.tables, tb.lens, tb.rows, block_size=tb.block_size, Hkv=tb.k_store.shape[1], G=G,
+                          chunk_tiles=chunk_tiles, shared_chunk_tiles=min(SHARED_MAX_TILES, 2 * chunk_tiles),
+                          shared_min_groups=min_groups)
     out = ops.tree_decode(tb.q, tb.k_store, tb.v_store, block_tables=tb.block_tables, plan=plan, scale=tb.scale)
     torch.cuda.synchronize()
     return out, plan
@@ -51,13 +55,14 @@ def _close(got, want, what):
     assert err.max() <= 0, (what, float(np.abs(got - want).max()))
 
 
-@pytest.mark.parametrize("min_groups", [3, 1, 99])
-def test_tree_decode_qwen3_8b_trees(gpu, min_groups):
+@pytest.mark.parametrize("min_groups,defaults", [(3, False), (1, False), (99, False), (3, True)])
+def test_tree_decode_qwen3_8b_trees(gpu, min_groups, defaults):
     """4 trees x 32 leaves over 2048-token prompts, Qwen3-8B attention shapes; shared
-    tasks for chunks of >= min_groups member groups (1: all, 99: none)."""
-    print(f"case tree qwen3-8b full min_groups={min_groups}", flush=True)
+    tasks of up to 32 tiles for chunks of >= min_groups member groups (1: all, 99: none),
+    and the default plan."""
+    print(f"case tree qwen3-8b full min_groups={min_groups} defaults={defaults}", flush=True)
     tb = prefix_tree_batch(device="cuda", seed=0)
-    out, plan = _run_tree(tb, min_groups=min_groups)
+    out, plan = _run_tree(tb, min_groups=min_groups, defaults=defaults)
     assert plan.unique_tokens() < 0.1 * tb.logical_tokens()
     rows_t = torch.tensor(tb.rows, dtype=torch.int32, device="cuda")
     ref = ops.paged_decode(tb.q, tb.k_store, tb.v_store, max_seqlen=max(tb.lens), block_tables=tb.block_tables,
