@@ -8,7 +8,7 @@
 //
 // A kv head's query rows are numbered r = position * G + g (g = head within
 // the group). A workgroup takes kPfRows consecutive rows of one (batch, kv
-// head): each of its 4 wavefronts owns kPfCols 16-column MFMA tiles (S^T =
+// head): each of its 8 wavefronts owns kPfCols 16-column MFMA tiles (S^T =
 // K.Q^T on v_mfma 16x16x32, online softmax in base 2 with a lazy rescale,
 // O += P.V, as in the decode kernels); tiles with no visible key in a step
 // skip it. The workgroup streams the kPfKeys-key K/V stages its rows need
@@ -18,9 +18,12 @@
 // = 4 keys per write), which is the P.V operand layout. A stage is computed in
 // 32-key steps (two S^T chains, one softmax update, P.V on 16x16x32). Loads
 // are unconditional (the token index is clamped into the sequence) and values
-// of tokens past the sequence end are replaced by zeros. One tile per
-// wavefront and 32-key stages measured fastest (more tiles per wavefront
-// raise register use to one wavefront per SIMD).
+// of tokens past the sequence end are replaced by zeros. Score masking runs
+// only on key blocks some column cannot fully see, and the softmax scale
+// rides in the exponent's fma. One tile per wavefront, 8 wavefronts and
+// 64-key stages measured fastest (more tiles per wavefront raise register use
+// to one wavefront per SIMD; 4 wavefronts or 32-key stages re-stage K/V for
+// fewer rows; 128-key stages halve the resident workgroups).
 #include "mentat_common.h"
 
 namespace mentat {
@@ -68,7 +71,7 @@ struct PrefillParams {
   float scale_log2;
 };
 
-constexpr int kPfWaves = 4;
+constexpr int kPfWaves = 8;
 constexpr int kPfThreads = 64 * kPfWaves;
 constexpr int kPfCols = 1;                         // 16-row column tiles per wavefront
 constexpr int kPfRows = 16 * kPfCols * kPfWaves;  // query rows per workgroup
@@ -76,7 +79,7 @@ constexpr float kPfSlack = 8.f;
 
 // LDS stage of kPfKeys keys: K rows (one token, padded by 16 bytes) and V^T
 // rows (one dim's kPfKeys tokens, padded by 8 bytes).
-constexpr int kPfKeys = 32;
+constexpr int kPfKeys = 64;
 template <int D> struct PfLds {
   static constexpr int KRS = 2 * D + 16;
   static constexpr int VRS = 2 * kPfKeys + 8;
@@ -110,6 +113,8 @@ __global__ __launch_bounds__(kPfThreads) void prefill_attn_kernel(PrefillParams 
   // Column tile c of this wave: rows rw + 16c + lr -> position, head.
   const int rw = r0 + 16 * NC * wave;
   int tpos_hi[NC], tkey_lo[NC];   // per tile (wave-uniform): last position, first key
+  int tpos_lo[NC], tkmin_hi[NC];  // per tile: first position, the latest first key of its columns
+  bool tfull[NC];                 // per tile: all 16 columns are rows of the sequence
   int qpos[NC], kmin[NC];         // per lane's column
   bool col_ok[NC];
   uint4 qo[NC][KS];
@@ -120,6 +125,9 @@ __global__ __launch_bounds__(kPfThreads) void prefill_attn_kernel(PrefillParams 
     const int rt = rw + 16 * c;
     tpos_hi[c] = rt < rows ? min((rt + 15) / G, p.S - 1) : -1;
     tkey_lo[c] = p.window > 0 ? min(rt / G, p.S - 1) - p.window + 1 : 0;
+    tpos_lo[c] = rt / G;
+    tkmin_hi[c] = p.window > 0 ? tpos_hi[c] - p.window + 1 : 0;
+    tfull[c] = rt + 15 < rows;
     const int row = rt + lr;
     col_ok[c] = row < rows;
     qpos[c] = col_ok[c] ? row / G : 0;
@@ -223,17 +231,27 @@ __global__ __launch_bounds__(kPfThreads) void prefill_attn_kernel(PrefillParams 
       static_for<NC>([&](auto c_) {
         constexpr int c = decltype(c_)::value;
         if (!live[c]) return;
+        // Raw scores; the scale is applied inside the exponent (one fma per score) and to the
+        // running maximum. Masking only where some column of the tile cannot see the whole
+        // 32-key block (the diagonal, the window's edge, the sequence's last rows).
         float sc[8];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const int ka = kb + 4 * lg + i, kc = ka + 16;
-          sc[i] = s0[c][i] * p.scale_log2;
-          sc[4 + i] = s1[c][i] * p.scale_log2;
-          if (!col_ok[c] || ka > qpos[c] || ka < kmin[c]) sc[i] = kNegInf;
-          if (!col_ok[c] || kc > qpos[c] || kc < kmin[c]) sc[4 + i] = kNegInf;
+          sc[i] = s0[c][i];
+          sc[4 + i] = s1[c][i];
+        }
+        const bool inside = tfull[c] && kb + 31 <= tpos_lo[c] && kb >= tkmin_hi[c];
+        if (!inside) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int ka = kb + 4 * lg + i, kc = ka + 16;
+            if (!col_ok[c] || ka > qpos[c] || ka < kmin[c]) sc[i] = kNegInf;
+            if (!col_ok[c] || kc > qpos[c] || kc < kmin[c]) sc[4 + i] = kNegInf;
+          }
         }
         float pm = fmaxf(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])),
                          fmaxf(fmaxf(sc[4], sc[5]), fmaxf(sc[6], sc[7])));
+        pm = pm == kNegInf ? kNegInf : pm * p.scale_log2;
         const bool grow = (m[c] == kNegInf) ? (pm != kNegInf) : (pm > m[c] + kPfSlack);
         if (__builtin_amdgcn_ballot_w64(grow)) {
           pm = fmaxf(pm, __shfl_xor(pm, 16));
@@ -253,8 +271,8 @@ __global__ __launch_bounds__(kPfThreads) void prefill_attn_kernel(PrefillParams 
         f32x4_t pa, pb;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          pa[i] = fast_exp2(sc[i] - ms);
-          pb[i] = fast_exp2(sc[4 + i] - ms);
+          pa[i] = fast_exp2(__builtin_fmaf(sc[i], p.scale_log2, -ms));
+          pb[i] = fast_exp2(__builtin_fmaf(sc[4 + i], p.scale_log2, -ms));
         }
         l[c] += ((pa[0] + pa[1]) + (pa[2] + pa[3])) + ((pb[0] + pb[1]) + (pb[2] + pb[3]));
         const uint2 ua = PMfma<T>::pack(pa), ub = PMfma<T>::pack(pb);
