@@ -88,16 +88,22 @@ class MentatBatchGenerator(MentatGenerator):
         prefill_before = prefill_s
         while live:
             # retire finished trees, refill their slots
+            active = {}
             for run in list(live):
-                if run.step >= self.max_new_tokens or not run.tree.get_active_leaves():
+                leaves = run.tree.get_active_leaves() if run.step < self.max_new_tokens else []
+                if not leaves:
                     done[run.index] = self._finish_tree(run)
                     live.remove(run)
+                else:
+                    active[id(run)] = leaves
             admit()
             if not live:
                 break
             batch, trees, steps, nacts, logs = [], [], [], [], []
             for run in live:
-                leaves = run.tree.get_active_leaves()
+                leaves = active.get(id(run))
+                if leaves is None:  # admitted above
+                    leaves = run.tree.get_active_leaves()
                 run.active_branch_trace.append(len(leaves))
                 run.decode_tokens += len(leaves)
                 batch += leaves

@@ -234,11 +234,17 @@ class MentatGenerator:
                          st.topk_ids.view(torch.float32)], dim=1)
         rec_cpu = rec.cpu().numpy()
         ids_cpu = np.ascontiguousarray(rec_cpu[:, 2 + self.K:2 + 2 * self.K]).view(np.int32)
+        # Python lists (the float32 values as Python floats) are far cheaper to
+        # index per leaf than numpy scalars.
+        K = self.K
+        rec_rows = rec_cpu.tolist()
+        id_rows = ids_cpu.tolist()
         for i, leaf in enumerate(leaves):
             if not leaf.is_active:
                 continue
             tree, step, num_active, log = trees[i], steps[i], num_actives[i], logs[i]
-            H = float(rec_cpu[i, 0])
+            row = rec_rows[i]
+            H = row[0]
             log.entropy_trace.append((step, leaf.node_id, H))
             if leaf.entropy_ema is None:
                 leaf.entropy_ema = H
@@ -251,11 +257,11 @@ class MentatGenerator:
                 open_gate = H > tau
             else:
                 open_gate = H > self.entropy_threshold
-            top_ids = [int(x) for x in ids_cpu[i]]
-            top_lps = [float(x) for x in rec_cpu[i, 2:2 + self.K]]
-            if open_gate and headroom >= self.K:
+            top_ids = id_rows[i]
+            top_lps = row[2:2 + K]
+            if open_gate and headroom >= K:
                 children = tree.branch_leaf(leaf, top_ids, top_lps)
-                log.branch_points.append((step, float(rec_cpu[i, 1]), len(children)))
+                log.branch_points.append((step, row[1], len(children)))
                 for child in children:
                     child.creation_step = step
                     self._handle_eos(tree, child)

@@ -394,13 +394,14 @@ class PagedKVCacheManager:
                       and s.tokens_in_last_block.count(s.tokens_in_last_block[0]) == L for s in seqs)
         tails = []
         if uniform:
-            tails0 = [s.page_table[0][-1] if s.page_table[0] else -1 for s in seqs]
+            pts = [s.page_table for s in seqs]
+            tails0 = [pt[0][-1] if pt[0] else -1 for pt in pts]
             rc0 = [rc[t] if t >= 0 else 0 for t in tails0]
             shared0 = any(r > 1 for r in rc0)
             ngroups0 = len(set(tails0))
             tails.append(tails0)
             for l in range(1, L):
-                tl = [s.page_table[l][-1] if s.page_table[l] else -1 for s in seqs]
+                tl = [pt[l][-1] if pt[l] else -1 for pt in pts]
                 if [rc[t] if t >= 0 else 0 for t in tl] != rc0:
                     uniform = False
                     break
@@ -420,8 +421,9 @@ class PagedKVCacheManager:
         cow_at = [i for i in range(N) if p0[2, i] >= 0]
         events = sorted([(i, 0) for i in new_at] + [(i, 1) for i in cow_at])
         alloc, release = self.allocator.alloc, self.allocator.release
+        plan[1:, 1:] = p0[1:]
+        plan[1:, 2] = -1
         for l in range(1, L):
-            cows = [-1] * N
             dst = tails[l]  # the tail pages, replaced below where an event gives a new one
             for i, kind in events:
                 table = seqs[i].page_table[l]
@@ -433,12 +435,9 @@ class PagedKVCacheManager:
                     dst[i] = alloc()
                     release(old)
                     table[-1] = dst[i]
-                    cows[i] = old
-            pl = plan[l]
-            pl[0] = dst
-            pl[1] = p0[1]
-            pl[2] = cows
-            pl[3:] = p0[3:]
+                    plan[l, 2, i] = old
+        if L > 1:
+            plan[1:, 0] = tails[1:]  # one conversion for every layer's destinations
         # Layer 0's counters are the step's counters for every layer.
         for s in seqs:
             s.tokens_in_last_block[1:] = [s.tokens_in_last_block[0]] * (L - 1)
