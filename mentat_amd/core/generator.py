@@ -210,7 +210,12 @@ class MentatGenerator:
         if flat.size == 0:
             flat = np.zeros(1, dtype=np.int32)
         dev = self.wrapper.device
-        return torch.from_numpy(off).to(dev), torch.from_numpy(flat).to(dev)
+        if dev.type != "cuda":
+            return torch.from_numpy(off).to(dev), torch.from_numpy(flat).to(dev)
+        # Pinned staging: the uploads and the row kernel queue behind the step's
+        # decode without a host round trip.
+        return (torch.from_numpy(off).pin_memory().to(dev, non_blocking=True),
+                torch.from_numpy(flat).pin_memory().to(dev, non_blocking=True))
 
     def _decide(self, tree: PrefixTree, leaves: list[TreeNode], logits: torch.Tensor, step: int,
                 num_active: int) -> None:

@@ -356,7 +356,7 @@ def semantic_similar_mask(vectors: list, parent_key: list, group: list, threshol
         _require(v.dtype == dt and v.device == dev and v.is_contiguous() and v.numel() == H,
                  "vectors must be contiguous, of one dtype, device and length")
     meta = torch.tensor([v.data_ptr() for v in vectors] + [int(k) for k in parent_key] + [int(g) for g in group],
-                        dtype=torch.int64).to(dev)
+                        dtype=torch.int64).pin_memory().to(dev, non_blocking=True)
     keys = meta[M:].to(torch.int32)
     scratch = torch.empty(M * H, dtype=dt, device=dev)
     mask = torch.empty(M * M, dtype=torch.uint8, device=dev)
