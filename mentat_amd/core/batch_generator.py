@@ -26,8 +26,10 @@ import math
 import time
 from dataclasses import dataclass, field
 
+import numpy as np
 import torch
 
+from .. import ops
 from .generator import MentatGenerator
 from .generator_utils import PrefixTree, TreeNode
 
@@ -116,8 +118,9 @@ class MentatBatchGenerator(MentatGenerator):
                                                               [l.seq_id for l in batch])
             self._total_tokens_decoded += len(batch)
             self._update_semantic_vectors(batch, hidden)
+            ahead = self._similarity_ahead(live, batch, logs)
             self._decide_rows(batch, logits, trees, steps, nacts, logs)
-            self._prune_runs(live)
+            self._prune_runs(live, ahead)
             for run in live:
                 if self.step_hook is not None:
                     self.step_hook(run.step, run.tree)
@@ -132,11 +135,39 @@ class MentatBatchGenerator(MentatGenerator):
         return [done[i] for i in range(len(prompts))]
 
     # ------------------------------------------------------------------
-    def _prune_runs(self, runs: list) -> None:
+    def _similarity_ahead(self, runs: list, batch: list, logs: list):
+        """The prune's similarity mask, queued before the step's decisions.
+
+        Exact when min_steps_before_prune >= 1: after the decisions, a tree's
+        eligible leaves are its eligible batch leaves that are still active
+        (branched and finished leaves are inactive; new children, created this
+        step, are too young), in the same depth-first order, with unchanged
+        vectors and parents. So the mask over the batch's eligible leaves,
+        restricted to the survivors, is the mask the prune would compute after
+        the decisions. Its copy completes with the decision record's. Returns
+        None when the rule does not apply (the prune then computes its own)."""
+        if self.min_steps_before_prune < 1 or self.wrapper.device.type != "cuda":
+            return None
+        gi_of = {id(run): gi for gi, run in enumerate(runs)}
+        sv, groups = [], []
+        for leaf, run in zip(batch, logs):
+            if leaf.semantic_vector is not None and run.step - leaf.creation_step >= self.min_steps_before_prune:
+                sv.append(leaf)
+                groups.append(gi_of[id(run)])
+        if len(sv) <= 1:
+            return sv, groups, None
+        mask = ops.semantic_similar_mask([l.semantic_vector for l in sv], self._similar_keys(sv), groups,
+                                         self.semantic_similarity_threshold, wait=False)
+        return sv, groups, mask
+
+    def _prune_runs(self, runs: list, ahead=None) -> None:
         """Every tree's semantic-similarity prune (the rule of _prune_similar, per
         tree) from one similarity matrix over all trees' eligible leaves: pairs
         are kept only within a tree, so each tree sees exactly its own pairs, in
         its own row-major order."""
+        if ahead is not None:
+            self._prune_runs_ahead(runs, *ahead)
+            return
         all_sv, groups, per = [], [], []
         for gi, run in enumerate(runs):
             leaves = run.tree.get_active_leaves()
@@ -158,6 +189,33 @@ class MentatBatchGenerator(MentatGenerator):
             pairs = by_group.get(gi)
             if pairs:
                 self._apply_prune(run.tree, sv, [(i - base, j - base) for i, j in pairs], run.step, run)
+
+    def _prune_runs_ahead(self, runs: list, sv: list, groups: list, mask) -> None:
+        """_prune_runs from the mask of _similarity_ahead (see there)."""
+        # Survivors are active leaves of their tree, so two or more of them also
+        # satisfy the rule's "more than one active leaf".
+        local = [-1] * len(sv)          # index among the tree's surviving eligible leaves
+        members: list = [[] for _ in runs]
+        for i, leaf in enumerate(sv):
+            if leaf.is_active:
+                members[groups[i]].append(i)
+        per = [[] for _ in runs]
+        for g, idx in enumerate(members):
+            if len(idx) <= 1:
+                continue
+            for k, i in enumerate(idx):
+                local[i] = k
+            per[g] = [sv[i] for i in idx]
+        if mask is None or not any(per):
+            return
+        ii, jj = np.nonzero(mask.numpy())
+        by_group: dict = {}
+        for i, j in zip(ii.tolist(), jj.tolist()):
+            if local[i] >= 0 and local[j] >= 0:
+                by_group.setdefault(groups[i], []).append((local[i], local[j]))
+        for g, pairs in by_group.items():
+            run = runs[g]
+            self._apply_prune(run.tree, per[g], pairs, run.step, run)
 
     def _start_tree(self, idx: int, prompt) -> _TreeRun:
         dev = self.wrapper.device

@@ -356,18 +356,24 @@ class MentatGenerator:
         if pruned:
             log.diversity_pruning_events.append((step, pruned))
 
-    def _similar_pairs(self, sv_leaves: list[TreeNode], groups: list) -> list:
-        """(i, j), i < j, row-major: leaves of the same group (tree) whose semantic
-        vectors have cosine similarity above the threshold and that are not
-        siblings (reference :447-460). The mask is one device call
-        (ops.semantic_similar_mask: F.normalize + product in the vectors' dtype,
-        triangle, sibling and group masks) read back as M*M bytes."""
+    def _similar_keys(self, sv_leaves: list[TreeNode]) -> list:
+        """Sibling keys: leaves with one parent share a key; a parentless leaf
+        gets a key of its own."""
         keys, parents = [], {}
         for i, leaf in enumerate(sv_leaves):
             if leaf.parent is None:
                 keys.append(-1 - i)  # never equal to another leaf's key
             else:
                 keys.append(parents.setdefault(id(leaf.parent), len(parents)))
+        return keys
+
+    def _similar_pairs(self, sv_leaves: list[TreeNode], groups: list) -> list:
+        """(i, j), i < j, row-major: leaves of the same group (tree) whose semantic
+        vectors have cosine similarity above the threshold and that are not
+        siblings (reference :447-460). The mask is one device call
+        (ops.semantic_similar_mask: F.normalize + product in the vectors' dtype,
+        triangle, sibling and group masks) read back as M*M bytes."""
+        keys = self._similar_keys(sv_leaves)
         mask = ops.semantic_similar_mask([l.semantic_vector for l in sv_leaves], keys, groups,
                                          self.semantic_similarity_threshold)
         ii, jj = np.nonzero(mask)

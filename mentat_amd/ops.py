@@ -341,13 +341,16 @@ def semantic_ema(vectors: list, hidden: torch.Tensor, fresh: list, alpha: float)
     check(st, "mentat_semantic_ema")
 
 
-def semantic_similar_mask(vectors: list, parent_key: list, group: list, threshold: float) -> np.ndarray:
+def semantic_similar_mask(vectors: list, parent_key: list, group: list, threshold: float,
+                          wait: bool = True):
     """Host bool [M, M]: entry (i, j) is set iff i < j, same group, different
     parent key, and the cosine similarity of the two vectors (F.normalize +
-    mm in their dtype) exceeds ``threshold``."""
+    mm in their dtype) exceeds ``threshold``. With ``wait=False`` the mask is
+    returned as a pinned uint8 [M, M] tensor whose copy is still in flight on
+    the current stream (read it after that stream's next synchronisation)."""
     M = len(vectors)
     if M == 0:
-        return np.zeros((0, 0), dtype=bool)
+        return np.zeros((0, 0), dtype=bool) if wait else torch.zeros(0, 0, dtype=torch.uint8)
     dev, dt = vectors[0].device, vectors[0].dtype
     H = vectors[0].numel()
     _require(dev.type == "cuda", "semantic_similar_mask runs on the GPU only")
@@ -364,6 +367,10 @@ def semantic_similar_mask(vectors: list, parent_key: list, group: list, threshol
                                            DTYPE_CODES[dt], ptr(scratch), scratch.numel() * scratch.element_size(),
                                            ptr(mask), stream_handle(dev))
     check(st, "mentat_semantic_similar")
+    if not wait:
+        host = torch.empty(M * M, dtype=torch.uint8, pin_memory=True)
+        host.copy_(mask, non_blocking=True)
+        return host.view(M, M)
     return mask.cpu().numpy().reshape(M, M).astype(bool)
 
 

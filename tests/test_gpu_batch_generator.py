@@ -25,23 +25,30 @@ def _prompts():
     return [np.random.default_rng(s).integers(0, 32000, 40 + 7 * s).tolist() for s in range(3)]
 
 
-@pytest.mark.parametrize("gate,thr", [("relative", 2.0), ("absolute", 2.0)])
-def test_batched_rollouts_match_single_prompt_rollouts(gpu, gate, thr):
+@pytest.mark.parametrize("gate,thr,sim", [("relative", 2.0, None), ("absolute", 2.0, None),
+                                          ("absolute", 1.5, 0.2), ("absolute", 1.5, 0.5)])
+def test_batched_rollouts_match_single_prompt_rollouts(gpu, gate, thr, sim):
+    """sim: a semantic-similarity threshold low enough that leaves are pruned
+    (the batch queues its similarity mask before the step's decisions; the
+    single-prompt generator computes it after them)."""
     import make_cfg1_trajectory as mk
     from mentat_amd.core.batch_generator import MentatBatchGenerator
     from mentat_amd.core.generator import MentatGenerator
 
-    print(f"case batch generator gate={gate}", flush=True)
+    print(f"case batch generator gate={gate} thr={thr} sim={sim}", flush=True)
     model = mk.build_model().to("cuda")
     prompts = _prompts()
+    knobs = dict(KNOBS)
+    if sim is not None:
+        knobs["semantic_similarity_threshold"] = sim
     singles = []
     with torch.no_grad():
         for ids in prompts:
-            g = MentatGenerator(model, mk.StubTokenizer(ids), gate=gate, entropy_threshold=thr, **KNOBS)
+            g = MentatGenerator(model, mk.StubTokenizer(ids), gate=gate, entropy_threshold=thr, **knobs)
             res = g.generate("stub")
             singles.append((res, g.get_diagnostics()))
             assert g.kv_cache_mgr.allocator.num_used == 0
-        bg = MentatBatchGenerator(model, mk.StubTokenizer(prompts[0]), gate=gate, entropy_threshold=thr, **KNOBS)
+        bg = MentatBatchGenerator(model, mk.StubTokenizer(prompts[0]), gate=gate, entropy_threshold=thr, **knobs)
         batched = bg.generate_batch(prompts, max_trees=2)
     diag = bg.get_batch_diagnostics()
     assert bg.kv_cache_mgr.allocator.num_used == 0
@@ -53,6 +60,7 @@ def test_batched_rollouts_match_single_prompt_rollouts(gpu, gate, thr):
         pd = diag["prompts"][p]
         assert [tuple(x[::2]) for x in pd["branch_points"]] == [tuple(x[::2]) for x in d["branch_points"]], p
         assert pd["active_branch_trace"] == d["active_branch_trace"], p
+        assert pd["diversity_pruning_events"] == d["diversity_pruning_events"], p
         assert len(pd["entropy_trace"]) == len(d["entropy_trace"])
         for (s1, n1, h1), (s2, n2, h2) in zip(pd["entropy_trace"], d["entropy_trace"]):
             assert (s1, n1) == (s2, n2) and abs(h1 - h2) < 1e-4
@@ -60,6 +68,8 @@ def test_batched_rollouts_match_single_prompt_rollouts(gpu, gate, thr):
     single_max = max(max(d["active_branch_trace"] or [1]) for _, d in singles)
     assert max(bg.batch_trace) > single_max
     assert diag["decode_tokens_total"] == sum(sum(d["active_branch_trace"]) for _, d in singles)
+    if sim is not None:  # the case really pruned
+        assert sum(len(diag["prompts"][p]["diversity_pruning_events"]) for p in diag["prompts"]) > 0
 
 
 def test_cpu_rollout_restatement_follows_the_generator(gpu):
