@@ -396,13 +396,23 @@ class PagedKVCacheManager:
         if uniform:
             pts = [s.page_table for s in seqs]
             tails0 = [pt[0][-1] if pt[0] else -1 for pt in pts]
-            rc0 = [rc[t] if t >= 0 else 0 for t in tails0]
+            paged = -1 not in tails0   # every sequence has a page in layer 0 (decode)
+            rc0 = list(map(rc.__getitem__, tails0)) if paged else [rc[t] if t >= 0 else 0 for t in tails0]
             shared0 = any(r > 1 for r in rc0)
             ngroups0 = len(set(tails0))
             tails.append(tails0)
             for l in range(1, L):
-                tl = [pt[l][-1] if pt[l] else -1 for pt in pts]
-                if [rc[t] if t >= 0 else 0 for t in tl] != rc0:
+                if paged:
+                    try:
+                        tl = [pt[l][-1] for pt in pts]
+                    except IndexError:  # an empty table where layer 0 has pages
+                        uniform = False
+                        break
+                    rcl = list(map(rc.__getitem__, tl))
+                else:
+                    tl = [pt[l][-1] if pt[l] else -1 for pt in pts]
+                    rcl = [rc[t] if t >= 0 else 0 for t in tl]
+                if rcl != rc0:
                     uniform = False
                     break
                 if shared0 and not (len(set(tl)) == ngroups0 == len(set(zip(tails0, tl)))):
