@@ -44,9 +44,12 @@ template <> struct G16<F16> {
 constexpr int kNormThreads = 256;
 
 // One workgroup per row; each thread owns 8-element groups g = tid, tid + 256, ...
-// (H % 8 == 0, H <= 8 * 256 * kNormGroups).
+// (H % 8 == 0, H <= 8 * 256 * kNormGroups). NG: groups per thread; FULL: every
+// thread owns NG groups (H a multiple of 2048), so no load sits under a branch.
+// The weight is loaded with the row, before the block reduction, so the row
+// costs one memory round trip.
 constexpr int kNormGroups = 4;
-template <typename T>
+template <typename T, int NG, bool FULL>
 __global__ __launch_bounds__(kNormThreads) void rmsnorm_kernel(const uint16_t* x, const uint16_t* res_in,
                                                                uint16_t* res_out, const uint16_t* w, uint16_t* y,
                                                                int H, float eps) {
@@ -54,13 +57,15 @@ __global__ __launch_bounds__(kNormThreads) void rmsnorm_kernel(const uint16_t* x
   const int row = blockIdx.x, tid = threadIdx.x;
   const long base = (long)row * H;
   const int ng = H / 8;
-  float h[kNormGroups][8];
+  float h[NG][8];
+  uint4 wv[NG];
   float ss = 0.f;
 #pragma unroll
-  for (int k = 0; k < kNormGroups; ++k) {
+  for (int k = 0; k < NG; ++k) {
     const int g = tid + k * kNormThreads;
-    if (g < ng) {
+    if (FULL || g < ng) {
       const uint4 xv = *(const uint4*)(x + base + 8 * g);
+      wv[k] = *(const uint4*)(w + 8 * g);
       const uint32_t xs[4] = {xv.x, xv.y, xv.z, xv.w};
       if (res_in) {
         const uint4 rv = *(const uint4*)(res_in + base + 8 * g);
@@ -93,11 +98,10 @@ __global__ __launch_bounds__(kNormThreads) void rmsnorm_kernel(const uint16_t* x
   for (int i = 0; i < kNormThreads / 64; ++i) tot += red[i];
   const float r = __frsqrt_rn(tot / (float)H + eps);
 #pragma unroll
-  for (int k = 0; k < kNormGroups; ++k) {
+  for (int k = 0; k < NG; ++k) {
     const int g = tid + k * kNormThreads;
-    if (g < ng) {
-      const uint4 wv = *(const uint4*)(w + 8 * g);
-      const uint32_t ws[4] = {wv.x, wv.y, wv.z, wv.w};
+    if (FULL || g < ng) {
+      const uint32_t ws[4] = {wv[k].x, wv[k].y, wv[k].z, wv[k].w};
       uint32_t o[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
@@ -107,6 +111,28 @@ __global__ __launch_bounds__(kNormThreads) void rmsnorm_kernel(const uint16_t* x
       }
       *(uint4*)(y + base + 8 * g) = make_uint4(o[0], o[1], o[2], o[3]);
     }
+  }
+}
+
+template <typename T, int NG>
+void launch_rmsnorm(int rows, int H, hipStream_t s, const uint16_t* xi, const uint16_t* ri, uint16_t* ro,
+                    const uint16_t* wi, uint16_t* yo, float eps) {
+  if ((H / 8) % kNormThreads == 0)
+    hipLaunchKernelGGL((rmsnorm_kernel<T, NG, true>), dim3(rows), dim3(kNormThreads), 0, s, xi, ri, ro, wi, yo, H,
+                       eps);
+  else
+    hipLaunchKernelGGL((rmsnorm_kernel<T, NG, false>), dim3(rows), dim3(kNormThreads), 0, s, xi, ri, ro, wi, yo,
+                       H, eps);
+}
+
+template <typename T>
+void launch_rmsnorm_t(int rows, int H, hipStream_t s, const uint16_t* xi, const uint16_t* ri, uint16_t* ro,
+                      const uint16_t* wi, uint16_t* yo, float eps) {
+  switch ((H / 8 + kNormThreads - 1) / kNormThreads) {
+    case 1: launch_rmsnorm<T, 1>(rows, H, s, xi, ri, ro, wi, yo, eps); break;
+    case 2: launch_rmsnorm<T, 2>(rows, H, s, xi, ri, ro, wi, yo, eps); break;
+    case 3: launch_rmsnorm<T, 3>(rows, H, s, xi, ri, ro, wi, yo, eps); break;
+    default: launch_rmsnorm<T, 4>(rows, H, s, xi, ri, ro, wi, yo, eps); break;
   }
 }
 
@@ -202,10 +228,10 @@ extern "C" int mentat_rmsnorm(const void* x, const void* residual_in, void* resi
   auto* yo = (uint16_t*)out;
   switch (dtype) {
     case MENTAT_BF16:
-      hipLaunchKernelGGL(rmsnorm_kernel<BF16>, dim3(rows), dim3(kNormThreads), 0, s, xi, ri, ro, wi, yo, H, eps);
+      launch_rmsnorm_t<BF16>(rows, H, s, xi, ri, ro, wi, yo, eps);
       break;
     case MENTAT_F16:
-      hipLaunchKernelGGL(rmsnorm_kernel<F16>, dim3(rows), dim3(kNormThreads), 0, s, xi, ri, ro, wi, yo, H, eps);
+      launch_rmsnorm_t<F16>(rows, H, s, xi, ri, ro, wi, yo, eps);
       break;
     default:
       return MENTAT_EUNSUP;
