@@ -151,6 +151,22 @@ __device__ __forceinline__ void put_shared(float* p, float v) {
 __device__ __forceinline__ float get_shared(const float* p) {
   return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+// The same device coherence for 16-byte pieces of partial O: buffer accesses
+// with the cache policy of agent-scope atomics (sc1).
+constexpr int kCoherent = 16;
+typedef uint32_t pd_u32x4_t __attribute__((ext_vector_type(4)));
+// Partial O of a split unit is stored row by row with column lr + 16 j at
+// position lr * NT + j, so a lane's NT values are contiguous (16-byte stores);
+// the merge maps a position back to its column.
+template <int D>
+__device__ __forceinline__ int partial_col(int pos) {
+  constexpr int NT = D / 16;
+  return pos / NT + 16 * (pos % NT);
+}
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t partial_rsrc(const NativeParams& p, int G, int D) {
+  const long bytes = ((long)p.N * p.Hkv + p.W) * G * D * (long)sizeof(float);
+  return make_rsrc(p.ws_o, (int)(bytes < 0x7fffffffL ? bytes : 0x7fffffffL));
+}
 
 // Pieces are the partial slots unit + w of waves w0..w1; lane l owns the
 // E = G*D/64 consecutive outputs starting at l*E of the unit's [G][D] block.
@@ -165,6 +181,7 @@ __device__ __forceinline__ void merge_unit(const NativeParams& p, int seq, int h
   const int g = (lane * E) / D;
   const int d0 = (lane * E) - g * D;
   const int n = w1 - w0 + 1;
+  const __amdgpu_buffer_rsrc_t rw = partial_rsrc(p, G, D);
   float M = kNegInf, L = 0.f, acc[E];
 #pragma unroll
   for (int e = 0; e < E; ++e) acc[e] = 0.f;
@@ -175,9 +192,19 @@ __device__ __forceinline__ void merge_unit(const NativeParams& p, int seq, int h
       const long slot = unit + w0 + min(k0 + (int)i, n - 1);
       mk[i] = get_shared(p.ws_ml + (slot * G + g) * 2);
       lk[i] = get_shared(p.ws_ml + (slot * G + g) * 2 + 1);
-      const float* wo = p.ws_o + (slot * G + g) * D + d0;
+      if constexpr (E % 4 == 0) {
+        const int off = (int)(((slot * G + g) * D + d0) * (long)sizeof(float));
 #pragma unroll
-      for (int e = 0; e < E; ++e) ok[i][e] = get_shared(wo + e);
+        for (int e = 0; e < E; e += 4) {
+          const pd_u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(rw, off + 4 * e, 0, kCoherent);
+#pragma unroll
+          for (int c = 0; c < 4; ++c) ok[i][e + c] = __uint_as_float(v[c]);
+        }
+      } else {
+        const float* wo = p.ws_o + (slot * G + g) * D + d0;
+#pragma unroll
+        for (int e = 0; e < E; ++e) ok[i][e] = get_shared(wo + e);
+      }
     });
     float Mn = M;
     static_for<KB>([&](auto i) {
@@ -197,9 +224,9 @@ __device__ __forceinline__ void merge_unit(const NativeParams& p, int seq, int h
     M = Mn;
   }
   const float inv = L > 0.f ? 1.f / L : 0.f;
-  const long ob = ((long)seq * p.Hq + (long)head * G + g) * D + d0;
+  const long ob = ((long)seq * p.Hq + (long)head * G + g) * D;
 #pragma unroll
-  for (int e = 0; e < E; ++e) Elem<T>::store1(p.out, ob + e, acc[e] * inv);
+  for (int e = 0; e < E; ++e) Elem<T>::store1(p.out, ob + partial_col<D>(d0 + e), acc[e] * inv);
 }
 
 template <typename T, int D, int G, int B>
@@ -378,13 +405,18 @@ __global__ __launch_bounds__(kNativeThreads) void paged_decode_mfma_kernel(Nativ
       }
     } else {
       const long slot = unit + wv;
+      const __amdgpu_buffer_rsrc_t rw = partial_rsrc(p, G, D);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int qrow = 4 * lg + i;
         if (qrow < G) {
-          float* wo = p.ws_o + (slot * G + qrow) * D + lr;
+          const int off = (int)(((slot * G + qrow) * D + lr * NT) * (long)sizeof(float));
 #pragma unroll
-          for (int j = 0; j < NT; ++j) put_shared(wo + 16 * j, o[j][i]);
+          for (int j = 0; j < NT; j += 4) {
+            const pd_u32x4_t v = {__float_as_uint(o[j][i]), __float_as_uint(o[j + 1][i]),
+                                  __float_as_uint(o[j + 2][i]), __float_as_uint(o[j + 3][i])};
+            __builtin_amdgcn_raw_buffer_store_b128(v, rw, off + 4 * j, 0, kCoherent);
+          }
         }
       }
       if (lane < G) {
