@@ -156,12 +156,13 @@ __device__ __forceinline__ float get_shared(const float* p) {
 constexpr int kCoherent = 16;
 typedef uint32_t pd_u32x4_t __attribute__((ext_vector_type(4)));
 // Partial O of a split unit is stored row by row with column lr + 16 j at
-// position lr * NT + j, so a lane's NT values are contiguous (16-byte stores);
-// the merge maps a position back to its column.
+// position 64 (j / 4) + 4 lr + j % 4: a lane's columns j .. j + 3 are one
+// 16-byte store and the 16 lanes of a row write 256 contiguous bytes per
+// instruction; the merge maps a position back to its column.
+__device__ __forceinline__ int partial_pos(int lr, int j) { return 64 * (j >> 2) + 4 * lr + (j & 3); }
 template <int D>
 __device__ __forceinline__ int partial_col(int pos) {
-  constexpr int NT = D / 16;
-  return pos / NT + 16 * (pos % NT);
+  return ((pos >> 2) & 15) + 16 * (4 * (pos >> 6) + (pos & 3));
 }
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t partial_rsrc(const NativeParams& p, int G, int D) {
   const long bytes = ((long)p.N * p.Hkv + p.W) * G * D * (long)sizeof(float);
@@ -410,12 +411,12 @@ __global__ __launch_bounds__(kNativeThreads) void paged_decode_mfma_kernel(Nativ
       for (int i = 0; i < 4; ++i) {
         const int qrow = 4 * lg + i;
         if (qrow < G) {
-          const int off = (int)(((slot * G + qrow) * D + lr * NT) * (long)sizeof(float));
+          const int off = (int)(((slot * G + qrow) * D) * (long)sizeof(float));
 #pragma unroll
           for (int j = 0; j < NT; j += 4) {
             const pd_u32x4_t v = {__float_as_uint(o[j][i]), __float_as_uint(o[j + 1][i]),
                                   __float_as_uint(o[j + 2][i]), __float_as_uint(o[j + 3][i])};
-            __builtin_amdgcn_raw_buffer_store_b128(v, rw, off + 4 * j, 0, kCoherent);
+            __builtin_amdgcn_raw_buffer_store_b128(v, rw, off + 4 * partial_pos(lr, j), 0, kCoherent);
           }
         }
       }
