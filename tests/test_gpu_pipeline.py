@@ -35,14 +35,22 @@ def _model(kind):
 
 @pytest.mark.parametrize("kind", ["qwen3", "llama"])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-def test_paged_decode_matches_dense_forward(gpu, kind, dtype):
-    print(f"case pipeline {kind} {dtype}", flush=True)
+@pytest.mark.parametrize("capture", [False, True])
+def test_paged_decode_matches_dense_forward(gpu, kind, dtype, capture):
+    """capture: decode steps as captured graphs; in bf16 these run the fused
+    layer glue (Llama: merged q/k/v and gate/up projections too; Qwen3 keeps its
+    QK-norm projections and takes the RoPE kernel on the split q/k)."""
+    print(f"case pipeline {kind} {dtype} capture={capture}", flush=True)
     cpu_model = _model(kind)
     gpu_model = _model(kind).to(device="cuda", dtype=dtype)
     adapter = get_adapter(gpu_model)
     kv = PagedKVCacheManager(num_layers=2, num_key_value_heads=2, head_dim=64, max_blocks=256, block_size=16,
                              device="cuda", dtype=dtype)
     wrapper = PagedModelWrapper(gpu_model, kv, adapter)
+    if capture:
+        wrapper.enable_step_capture()
+        assert wrapper.graphs.fused == (dtype == torch.bfloat16)
+        assert wrapper.graphs.merged == (dtype == torch.bfloat16 and kind == "llama")
     rng = np.random.default_rng(0)
     prompt = rng.integers(0, 1000, 21).tolist()
     s0 = kv.allocate_sequence()
@@ -75,6 +83,8 @@ def test_paged_decode_matches_dense_forward(gpu, kind, dtype):
             extra = kv.fork_sequence(kids[0])
             seqs[extra] = list(seqs[kids[0]])
             kids.append(extra)
+    if capture:
+        assert wrapper.graphs.captures > 0
     for sid in kids:
         kv.free_sequence(sid)
     assert kv.allocator.num_used == 0
