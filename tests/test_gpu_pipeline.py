@@ -34,10 +34,10 @@ def _model(kind):
 
 
 @pytest.mark.parametrize("kind", ["qwen3", "llama"])
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("capture", [False, True])
 def test_paged_decode_matches_dense_forward(gpu, kind, dtype, capture):
-    """capture: decode steps as captured graphs; in bf16 these run the fused
+    """capture: decode steps as captured graphs; in bf16 / f16 these run the fused
     layer glue (Llama: merged q/k/v and gate/up projections too; Qwen3 keeps its
     QK-norm projections and takes the RoPE kernel on the split q/k)."""
     print(f"case pipeline {kind} {dtype} capture={capture}", flush=True)
@@ -49,8 +49,8 @@ def test_paged_decode_matches_dense_forward(gpu, kind, dtype, capture):
     wrapper = PagedModelWrapper(gpu_model, kv, adapter)
     if capture:
         wrapper.enable_step_capture()
-        assert wrapper.graphs.fused == (dtype == torch.bfloat16)
-        assert wrapper.graphs.merged == (dtype == torch.bfloat16 and kind == "llama")
+        assert wrapper.graphs.fused == (dtype != torch.float32)
+        assert wrapper.graphs.merged == (dtype != torch.float32 and kind == "llama")
     rng = np.random.default_rng(0)
     prompt = rng.integers(0, 1000, 21).tolist()
     s0 = kv.allocate_sequence()
