@@ -124,8 +124,15 @@ def _merge_linears(lins) -> torch.Tensor:
     return w
 
 
+# Layers in the first of a step's two captured graphs. The host plans those
+# layers' appends, starts the first graph, and plans the other layers while it
+# runs: their appends are read only by the second graph, whose inputs are
+# copied in after the first graph in stream order.
+SPLIT_LAYERS = 2
+
+
 class _Bucket:
-    __slots__ = ("n", "graph", "dev", "host", "host_np", "logits", "hidden", "version")
+    __slots__ = ("n", "graph", "graph2", "state", "dev", "host", "host_np", "logits", "hidden", "version")
 
 
 class DecodeGraphs:
@@ -199,18 +206,24 @@ class DecodeGraphs:
         plans[:, :, n:] = -1               # dst block -1: skipped by the append kernel
         plans[:, 6, n:] = 0
 
-    def _forward(self, buf: torch.Tensor, nb: int):
+    def _forward(self, buf: torch.Tensor, nb: int, lo: int = 0, hi=None, state=None):
+        """Layers lo .. hi - 1 of the step (all by default). The first range
+        starts from the embeddings; a range that ends before the last layer
+        returns the state the next range starts from, the last one returns
+        (logits, final hidden)."""
         if self.fused:
-            return self._forward_fused(buf, nb)
+            return self._forward_fused(buf, nb, lo, hi, state)
         a, m = self.a, self.m
         L = m.num_layers
+        hi = L if hi is None else hi
         ids = buf[0:nb].long().unsqueeze(0)            # [1, nb]
         pos = buf[nb:2 * nb].long().unsqueeze(1)       # [nb, 1]
         rows = buf[2 * nb:3 * nb]                      # [nb] int32
         plans = buf[3 * nb:].view(L, 7, nb)
         max_seqlen = m._pages_cap * m.block_size
-        hidden = a.embeddings(ids)
-        for layer_idx, block in enumerate(a.layers):
+        hidden = a.embeddings(ids) if lo == 0 else state
+        for layer_idx in range(lo, hi):
+            block = a.layers[layer_idx]
             attn = a.get_self_attn(block)
             residual = hidden
             x = a.apply_pre_attn_norm(block, hidden)
@@ -228,24 +241,32 @@ class DecodeGraphs:
             residual = hidden
             x = a.apply_pre_mlp_norm(block, hidden)
             hidden = a.apply_post_mlp_residual(block, residual, a.get_mlp(block)(x))
+        if hi < L:
+            return hidden
         hidden = a.final_norm(hidden).squeeze(0)
         return a.lm_head(hidden), hidden
 
-    def _forward_fused(self, buf: torch.Tensor, nb: int):
-        """_forward with the layer glue fused (see the module docstring)."""
+    def _forward_fused(self, buf: torch.Tensor, nb: int, lo: int = 0, hi=None, state=None):
+        """_forward with the layer glue fused (see the module docstring); the
+        state between layer ranges is (normalised input, residual stream)."""
         a, m = self.a, self.m
         L = m.num_layers
+        hi = L if hi is None else hi
         ids = buf[0:nb].long().unsqueeze(0)
         pos = buf[nb:2 * nb].long().unsqueeze(1)
         rows = buf[2 * nb:3 * nb]
         plans = buf[3 * nb:].view(L, 7, nb)
         max_seqlen = m._pages_cap * m.block_size
         layers = a.layers
-        hidden = a.embeddings(ids)                     # [1, nb, H]: the residual stream
-        ln = layers[0].input_layernorm
-        x, _ = ops.rmsnorm(hidden, ln.weight, ln.variance_epsilon)
+        if lo == 0:
+            hidden = a.embeddings(ids)                 # [1, nb, H]: the residual stream
+            ln = layers[0].input_layernorm
+            x, _ = ops.rmsnorm(hidden, ln.weight, ln.variance_epsilon)
+        else:
+            x, hidden = state
         Hq, Hk = a.num_attention_heads, a.num_key_value_heads
-        for layer_idx, block in enumerate(layers):
+        for layer_idx in range(lo, hi):
+            block = layers[layer_idx]
             attn = a.get_self_attn(block)
             if self.merged:
                 qkv = torch.nn.functional.linear(x, self._w_qkv[layer_idx])  # [1, nb, (Hq + 2 Hk) * D]
@@ -274,6 +295,8 @@ class DecodeGraphs:
             mlp_out = mlp.down_proj(act)
             ln = layers[layer_idx + 1].input_layernorm if layer_idx + 1 < L else a.final_norm
             x, hidden = ops.rmsnorm(mlp_out, ln.weight, ln.variance_epsilon, residual=hidden)
+        if hi < L:
+            return x, hidden
         x = x.squeeze(0)
         return a.lm_head(x), x
 
@@ -310,17 +333,27 @@ class DecodeGraphs:
                 self._forward(b.dev, nb)
         torch.cuda.current_stream(self.dev).wait_stream(s)
         g = torch.cuda.CUDAGraph()
+        g2 = None
+        k = self._split_layers()
         gc_on = gc.isenabled()
         gc.collect()
         gc.disable()
         try:
-            with torch.cuda.graph(g, stream=s):
-                b.logits, b.hidden = self._forward(b.dev, nb)
+            if k:
+                with torch.cuda.graph(g, stream=s):
+                    b.state = self._forward(b.dev, nb, 0, k)
+                g2 = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(g2, pool=g.pool(), stream=s):
+                    b.logits, b.hidden = self._forward(b.dev, nb, k, None, b.state)
+            else:
+                b.state = None
+                with torch.cuda.graph(g, stream=s):
+                    b.logits, b.hidden = self._forward(b.dev, nb)
         finally:
             if gc_on:
                 gc.enable()
         torch.cuda.current_stream(self.dev).wait_stream(s)
-        b.graph = g
+        b.graph, b.graph2 = g, g2
         b.version = m.tables_version
         self._graphs[nb] = b
         self.captures += 1
@@ -339,18 +372,44 @@ class DecodeGraphs:
             self._merge()           # weights were rebound: merge again, capture again
             self._graphs.clear()
         m = self.m
+        L = m.num_layers
         offsets = [m.get_kv_length(s) for s in seq_ids]  # RoPE positions: lengths before the append
         rows = [m._sequences[s].row for s in seq_ids]
-        plan = m.plan_append_step(seq_ids)                # [L, 7, n]
-        m._ensure_pages(int(plan[:, 4].max()) + 1)
+        k = self._split_layers()
+        st = m.plan_append_step_begin(seq_ids, max(k, 1))
+        # Overlap the later layers' planning with the first graph only when every
+        # layer's counters agree: then every layer's new token lands on the same
+        # page index, so the first layers' plan decides the table capacity.
+        overlap = bool(k) and st.get("uniform", False)
+        plan = st["plan"] if overlap else m.plan_append_step_finish(st)   # [L, 7, n]
+        m._ensure_pages(int(plan[:max(k, 1) if overlap else L, 4].max()) + 1)
         b = self._get(nb)
         h = b.host_np
-        L = m.num_layers
+        plans_h = h[3 * nb:].reshape(L, 7, nb)
         h[0:n] = token_ids
         h[nb:nb + n] = offsets
         h[2 * nb:2 * nb + n] = rows
-        h[3 * nb:].reshape(L, 7, nb)[:, :, :n] = plan
         self._fill_padding(h, nb, n)
-        b.dev.copy_(b.host, non_blocking=True)
-        b.graph.replay()
+        if overlap:
+            cut = 3 * nb + k * 7 * nb
+            plans_h[:k, :, :n] = plan[:k]
+            b.dev[:cut].copy_(b.host[:cut], non_blocking=True)
+            b.graph.replay()
+            plan = m.plan_append_step_finish(st)
+            if int(plan[k:, 4].max()) >= m._pages_cap:
+                raise RuntimeError("DecodeGraphs: a later layer's append needs more table pages than the first")
+            plans_h[k:, :, :n] = plan[k:]
+            b.dev[cut:].copy_(b.host[cut:], non_blocking=True)
+            b.graph2.replay()
+        else:
+            plans_h[:, :, :n] = plan
+            b.dev.copy_(b.host, non_blocking=True)
+            b.graph.replay()
+            if b.graph2 is not None:
+                b.graph2.replay()
         return b.logits[:n].clone(), b.hidden[:n].clone()
+
+    def _split_layers(self) -> int:
+        """Layers of the first graph (0: one graph for the whole step)."""
+        L = self.m.num_layers
+        return SPLIT_LAYERS if 0 < SPLIT_LAYERS < L else 0

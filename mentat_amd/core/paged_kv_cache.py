@@ -384,75 +384,109 @@ class PagedKVCacheManager:
         (counters, tail refcounts, sharing partition); if it does not hold the
         layers are planned one by one.
         """
+        return self.plan_append_step_finish(self.plan_append_step_begin(seq_ids))
+
+    def plan_append_step_begin(self, seq_ids: list[int], first_layers: int = 1) -> dict:
+        """First half of plan_append_step: layers 0 .. first_layers - 1 are
+        planned (``state["plan"][:first_layers]`` is final); plan_append_step_finish
+        plans the rest. Nothing else may touch the manager in between. A caller
+        can start the first layers' device work while the rest is planned."""
         L = self.num_layers
         N = len(seq_ids)
+        plan = np.empty((L, 7, N), dtype=np.int32)
+        st = {"seq_ids": seq_ids, "plan": plan, "next": L}
         if N == 0:
-            return np.zeros((L, 7, 0), dtype=np.int32)
+            return st
         seqs = [self._sequences[s] for s in seq_ids]
         rc = self.allocator.refcounts
+        # Every layer's counters equal layer 0's (else every layer is planned on its own).
         uniform = all(s.num_tokens.count(s.num_tokens[0]) == L
                       and s.tokens_in_last_block.count(s.tokens_in_last_block[0]) == L for s in seqs)
-        tails = []
-        if uniform:
-            pts = [s.page_table for s in seqs]
-            tails0 = [pt[0][-1] if pt[0] else -1 for pt in pts]
-            paged = -1 not in tails0   # every sequence has a page in layer 0 (decode)
-            rc0 = list(map(rc.__getitem__, tails0)) if paged else [rc[t] if t >= 0 else 0 for t in tails0]
-            shared0 = any(r > 1 for r in rc0)
-            ngroups0 = len(set(tails0))
-            tails.append(tails0)
-            for l in range(1, L):
-                if paged:
-                    try:
-                        tl = [pt[l][-1] for pt in pts]
-                    except IndexError:  # an empty table where layer 0 has pages
-                        uniform = False
-                        break
-                    rcl = list(map(rc.__getitem__, tl))
-                else:
-                    tl = [pt[l][-1] if pt[l] else -1 for pt in pts]
-                    rcl = [rc[t] if t >= 0 else 0 for t in tl]
-                if rcl != rc0:
-                    uniform = False
-                    break
-                if shared0 and not (len(set(tl)) == ngroups0 == len(set(zip(tails0, tl)))):
-                    uniform = False
-                    break
-                tails.append(tl)
-        if not uniform:
-            return np.stack([self.plan_append_batched(seq_ids, l) for l in range(L)])
-
-        plan = np.empty((L, 7, N), dtype=np.int32)
-        pages_before = [len(s.page_table[0]) for s in seqs]
+        pts = [s.page_table for s in seqs]
+        tails0 = [pt[0][-1] if pt[0] else -1 for pt in pts]
+        paged = -1 not in tails0   # every sequence has a page in layer 0 (decode)
+        rc0 = list(map(rc.__getitem__, tails0)) if paged else [rc[t] if t >= 0 else 0 for t in tails0]
+        pages_before = [len(pt[0]) for pt in pts]
         p0 = self.plan_append_batched(seq_ids, 0)
         plan[0] = p0
         # Layer 0's events, in batch order: a new tail page, and/or a copy-on-write.
-        new_at = [i for i, s in enumerate(seqs) if len(s.page_table[0]) > pages_before[i]]
+        new_at = [i for i, pt in enumerate(pts) if len(pt[0]) > pages_before[i]]
         cow_at = [i for i in range(N) if p0[2, i] >= 0]
-        events = sorted([(i, 0) for i in new_at] + [(i, 1) for i in cow_at])
+        st.update(seqs=seqs, pts=pts, uniform=uniform, paged=paged, tails0=tails0, rc0=rc0,
+                  shared0=any(r > 1 for r in rc0), ngroups0=len(set(tails0)), p0=p0,
+                  events=sorted([(i, 0) for i in new_at] + [(i, 1) for i in cow_at]), next=1)
+        self._plan_layers(st, min(max(first_layers, 1), L))
+        return st
+
+    def plan_append_step_finish(self, st: dict) -> np.ndarray:
+        """Second half of plan_append_step: the remaining layers; returns the
+        int32 [num_layers, 7, N] plans."""
+        self._plan_layers(st, self.num_layers)
+        return st["plan"]
+
+    def _plan_layers(self, st: dict, upto: int) -> None:
+        """Layers st["next"] .. upto - 1, in order. A layer whose structure is
+        layer 0's before the step (counters, tail refcounts, tail-sharing
+        partition) replays layer 0's new-page and copy-on-write events on its
+        own tables: the allocator calls plan_append_batched would make for it,
+        in the same order. Any other layer runs plan_append_batched itself.
+        Refcounts of a layer's blocks change only when that layer is planned,
+        so each check sees the layer as it was before the step."""
+        l0 = st["next"]
+        if l0 >= upto:
+            return
+        st["next"] = upto
+        plan, seqs, pts, rc = st["plan"], st["seqs"], st["pts"], self.allocator.refcounts
+        tails0, rc0, p0, events = st["tails0"], st["rc0"], st["p0"], st["events"]
         alloc, release = self.allocator.alloc, self.allocator.release
-        plan[1:, 1:] = p0[1:]
-        plan[1:, 2] = -1
-        for l in range(1, L):
-            dst = tails[l]  # the tail pages, replaced below where an event gives a new one
+        replayed = []
+        for l in range(l0, upto):
+            ok = st["uniform"]
+            tl = None
+            if ok:
+                if st["paged"]:
+                    try:
+                        tl = [pt[l][-1] for pt in pts]
+                    except IndexError:  # an empty table where layer 0 has pages
+                        ok = False
+                    if ok:
+                        ok = list(map(rc.__getitem__, tl)) == rc0
+                else:
+                    tl = [pt[l][-1] if pt[l] else -1 for pt in pts]
+                    ok = [rc[t] if t >= 0 else 0 for t in tl] == rc0
+                if ok and st["shared0"]:
+                    ok = len(set(tl)) == st["ngroups0"] == len(set(zip(tails0, tl)))
+            if not ok:
+                plan[l] = self.plan_append_batched(st["seq_ids"], l)
+                continue
+            pl = plan[l]
+            pl[1:] = p0[1:]
+            pl[2] = -1
             for i, kind in events:
-                table = seqs[i].page_table[l]
+                table = pts[i][l]
                 if kind == 0:
-                    dst[i] = alloc()
-                    table.append(dst[i])
+                    tl[i] = alloc()
+                    table.append(tl[i])
                 else:
                     old = table[-1]
-                    dst[i] = alloc()
+                    tl[i] = alloc()
                     release(old)
-                    table[-1] = dst[i]
-                    plan[l, 2, i] = old
-        if L > 1:
-            plan[1:, 0] = tails[1:]  # one conversion for every layer's destinations
-        # Layer 0's counters are the step's counters for every layer.
-        for s in seqs:
-            s.tokens_in_last_block[1:] = [s.tokens_in_last_block[0]] * (L - 1)
-            s.num_tokens[1:] = [s.num_tokens[0]] * (L - 1)
-        return plan
+                    table[-1] = tl[i]
+                    pl[2, i] = old
+            pl[0] = tl
+            replayed.append(l)
+        if replayed:
+            # Layer 0's counters are the step's counters for every replayed layer.
+            lo, hi = replayed[0], replayed[-1] + 1
+            if len(replayed) == hi - lo:
+                for s in seqs:
+                    s.tokens_in_last_block[lo:hi] = [s.tokens_in_last_block[0]] * (hi - lo)
+                    s.num_tokens[lo:hi] = [s.num_tokens[0]] * (hi - lo)
+            else:
+                for s in seqs:
+                    for l in replayed:
+                        s.tokens_in_last_block[l] = s.tokens_in_last_block[0]
+                        s.num_tokens[l] = s.num_tokens[0]
 
     def _launch_append(self, layer_idx: int, k: torch.Tensor, v: torch.Tensor, plan: np.ndarray) -> None:
         if plan.shape[1] == 0:

@@ -169,11 +169,14 @@ def test_find_blocked_tokens_closed_forms():
 
 
 @pytest.mark.parametrize("seed", range(6))
-def test_plan_append_step_equals_layer_by_layer_plans(seed):
-    """One decode step planned for all layers at once (plan_append_step) gives
-    the plans, block ids, refcounts, free set and counters of plan_append_batched
-    called layer by layer, on random traces with forks (shared tails, so
-    copy-on-write), frees and page boundaries; the oracle checks the same."""
+@pytest.mark.parametrize("first_layers", [0, 2, 5])
+def test_plan_append_step_equals_layer_by_layer_plans(seed, first_layers):
+    """One decode step planned for all layers at once (plan_append_step, or its
+    two halves with the first `first_layers` layers planned before the rest;
+    0: the one-call form) gives the plans, block ids, refcounts, free set and
+    counters of plan_append_batched called layer by layer, on random traces
+    with forks (shared tails, so copy-on-write), frees and page boundaries; the
+    oracle checks the same."""
     rng = random.Random(100 + seed)
     L, nb, B = 5, 4096, 4
     step = PagedKVCacheManager(L, 2, 16, max_blocks=nb, block_size=B, device="cpu", dtype=torch.float32)
@@ -205,7 +208,13 @@ def test_plan_append_step_equals_layer_by_layer_plans(seed):
             c.free(s)
         else:
             batch = rng.sample(live, rng.randint(1, len(live)))
-            got = step.plan_append_step(batch)
+            if first_layers:
+                st = step.plan_append_step_begin(batch, first_layers)
+                head = st["plan"][:first_layers].copy()
+                got = step.plan_append_step_finish(st)
+                assert (got[:first_layers] == head).all()   # the first layers were final
+            else:
+                got = step.plan_append_step(batch)
             want = np.stack([ref.plan_append_batched(batch, l) for l in range(L)])
             for l in range(L):
                 c.append_batched(batch, l, list(range(len(batch))))
@@ -237,3 +246,35 @@ def test_plan_append_step_non_uniform_layers_fall_back():
     want = np.stack([ref.plan_append_batched([0, 1], l) for l in range(L)])
     assert (got == want).all()
     assert step.allocator.refcounts == ref.allocator.refcounts
+
+
+@pytest.mark.parametrize("first_layers", [1, 2, 4])
+def test_plan_append_step_mixes_replay_and_layer_plans(first_layers):
+    """Equal counters in every layer but one layer whose tail is no longer
+    shared (its tail re-pointed at a private copy by hand): that layer is
+    planned on its own, the others replay layer 0, and the result is still the
+    layer-by-layer plans, ids and refcounts."""
+    L, B = 4, 4
+    mgrs = [PagedKVCacheManager(L, 2, 16, max_blocks=256, block_size=B, device="cpu", dtype=torch.float32)
+            for _ in range(2)]
+    for m in mgrs:
+        a = m.allocate_sequence()
+        for l in range(L):
+            m.plan_append(a, l, 6)
+        b = m.fork_sequence(a)
+        sb = m._sequences[b]
+        old = sb.page_table[2][-1]
+        new = m.allocator.alloc()
+        m.allocator.release(old)
+        sb.page_table[2][-1] = new
+    step, ref = mgrs
+    st = step.plan_append_step_begin([0, 1], first_layers)
+    got = step.plan_append_step_finish(st)
+    want = np.stack([ref.plan_append_batched([0, 1], l) for l in range(L)])
+    assert (got == want).all()
+    assert step.allocator.refcounts == ref.allocator.refcounts
+    assert step.allocator._free == ref.allocator._free
+    for sid in (0, 1):
+        s, r = step._sequences[sid], ref._sequences[sid]
+        assert (s.page_table, s.num_tokens, s.tokens_in_last_block) == (r.page_table, r.num_tokens,
+                                                                         r.tokens_in_last_block)
