@@ -1,4 +1,4 @@
-"""Captured decode steps: one HIP graph launch per batched decode forward.
+"""Captured decode steps: two HIP graph launches per batched decode forward.
 
 The eager decode step (PagedModelWrapper.decode_batch_tensor, the reference's
 core/generator_utils.py:340-418 loop) launches ~30 kernels per layer from
@@ -10,10 +10,13 @@ residuals, the final norm and the LM head — is captured once per batch-size
 bucket ``Nb`` and replayed per step.
 
 Per step the host does what must stay on the host: the allocator and page
-tables of every layer in one call (PagedKVCacheManager.plan_append_step, the
-same block ids as the per-layer loop), then one pinned host-to-device copy of
+tables of every layer (PagedKVCacheManager.plan_append_step_begin / _finish,
+the same block ids as the per-layer loop) and pinned host-to-device copies of
 the step's int32 inputs (token ids, RoPE positions, table rows and the
-[num_layers, 7, Nb] append plans) and one graph replay. Batches are padded to
+[num_layers, 7, Nb] append plans). The forward is captured as two graphs over
+one memory pool, the first SPLIT_LAYERS layers and the rest: the first graph
+starts once its layers are planned, and the other layers are planned while it
+runs and copied in before the second graph in stream order. Batches are padded to
 the bucket: padding entries carry the token 0 at position 0, read the
 manager's length-0 row (their attention output is zero) and have append plans
 whose destination block is -1, which the append kernel skips; their logits are
