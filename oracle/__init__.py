@@ -2,12 +2,13 @@
 
 This package restates, on the CPU, the reference algorithm that the HIP
 library replaces. Every function cites the reference file:line it follows.
-It is the checker, never the thing measured or shipped: only ``tests/``,
+It is what results are compared against, never the thing measured or
+shipped: only ``tests/``,
 ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``bench.py`` may
 import it. The product path (``mentat_amd``) never imports it.
 
 Modules
-  attention   build_packed_kv gather + per-sequence SDPA decode (fp64 checker
+  attention   build_packed_kv gather + per-sequence SDPA decode (fp64 oracle
               and the reference's own torch-CPU path for the CPU baseline)
   paged_cache BlockAllocator / SequenceState / PagedKVCacheManager bookkeeping
               (set-based allocator, fork/free, lazy copy-on-write append)
