@@ -51,8 +51,15 @@ def _wrapper(model, capture):
     return w
 
 
-def test_captured_steps_match_eager_steps(gpu):
-    print("case graph decode vs eager, bf16 2-layer llama", flush=True)
+@pytest.mark.parametrize("split", [1, 2])
+def test_captured_steps_match_eager_steps(gpu, monkeypatch, split):
+    """split: layers of the first of the step's two graphs (2 = the whole
+    2-layer model, one graph; 1 = two graphs, the second layer's append plans
+    made while the first graph runs)."""
+    from mentat_amd.core import graph_decode
+
+    monkeypatch.setattr(graph_decode, "SPLIT_LAYERS", split)
+    print(f"case graph decode vs eager, bf16 2-layer llama, split={split}", flush=True)
     model = _bf16_model()
     we, wg = _wrapper(model, False), _wrapper(model, True)
     rng = np.random.default_rng(0)
@@ -109,14 +116,18 @@ def test_captured_steps_match_eager_steps(gpu):
     used = {g.bucket(n) for n in sizes}
     assert len(used) >= 3, sizes                     # several buckets were replayed in turn
     assert g.captures == len(used), (g.captures, used)  # each captured once, then replayed
+    assert all((b.graph2 is not None) == (split < 2) for b in g._graphs.values())
 
 
 @pytest.mark.parametrize("gate,thr", [("absolute", 2.0)])
-def test_rollouts_with_and_without_capture(gpu, gate, thr):
+@pytest.mark.parametrize("split", [1, 2])
+def test_rollouts_with_and_without_capture(gpu, monkeypatch, gate, thr, split):
     import make_cfg1_trajectory as mk
+    from mentat_amd.core import graph_decode
     from mentat_amd.core.batch_generator import MentatBatchGenerator
 
-    print(f"case rollout capture on/off gate={gate}", flush=True)
+    monkeypatch.setattr(graph_decode, "SPLIT_LAYERS", split)
+    print(f"case rollout capture on/off gate={gate} split={split}", flush=True)
     model = mk.build_model().to("cuda")
     prompts = [np.random.default_rng(s).integers(0, 32000, 40 + 7 * s).tolist() for s in range(3)]
     knobs = dict(max_active_branches=6, branching_factor=3, max_new_tokens=24, block_size=16, max_blocks=4096,
