@@ -244,6 +244,10 @@ class MentatGenerator:
         K = self.K
         rec_rows = rec_cpu.tolist()
         id_rows = ids_cpu.tolist()
+        alpha, M = self.entropy_ema_alpha, self.M
+        keep = 1.0 - alpha
+        relative, thr = self.gate == "relative", self.entropy_threshold
+        is_eos = self.wrapper.is_eos
         for i, leaf in enumerate(leaves):
             if not leaf.is_active:
                 continue
@@ -254,25 +258,26 @@ class MentatGenerator:
             if leaf.entropy_ema is None:
                 leaf.entropy_ema = H
             else:
-                leaf.entropy_ema = self.entropy_ema_alpha * H + (1.0 - self.entropy_ema_alpha) * leaf.entropy_ema
-            headroom = self.M - num_active
-            if self.gate == "relative":
-                mult = adaptive_threshold(self.relative_entropy_multiplier, self.M, num_active)
+                leaf.entropy_ema = alpha * H + keep * leaf.entropy_ema
+            headroom = M - num_active
+            if relative:
+                mult = adaptive_threshold(self.relative_entropy_multiplier, M, num_active)
                 tau = leaf.entropy_ema * mult * self._soft_explore_factor(step)
                 open_gate = H > tau
             else:
-                open_gate = H > self.entropy_threshold
+                open_gate = H > thr
             top_ids = id_rows[i]
-            top_lps = row[2:2 + K]
             if open_gate and headroom >= K:
-                children = tree.branch_leaf(leaf, top_ids, top_lps)
+                children = tree.branch_leaf(leaf, top_ids, row[2:2 + K])
                 log.branch_points.append((step, row[1], len(children)))
                 for child in children:
                     child.creation_step = step
                     self._handle_eos(tree, child)
             else:
-                tree.extend_leaf(leaf, top_ids[0], top_lps[0])
-                self._handle_eos(tree, leaf)
+                tok = top_ids[0]
+                tree.extend_leaf(leaf, tok, row[2])
+                if is_eos(tok):
+                    self._handle_eos(tree, leaf)
 
     def _handle_eos(self, tree: PrefixTree, node: TreeNode) -> None:
         if self.wrapper.is_eos(node.token_ids[-1]):
