@@ -130,7 +130,9 @@ def _merge_linears(lins) -> torch.Tensor:
 # Layers in the first of a step's two captured graphs. The host plans those
 # layers' appends, starts the first graph, and plans the other layers while it
 # runs: their appends are read only by the second graph, whose inputs are
-# copied in after the first graph in stream order.
+# copied in after the first graph in stream order. At Llama-3-8B size two layers
+# of GPU work cover the other 30 layers' planning (one does not: 9.20 ms per
+# step at 144 leaves against 9.07 for two and three).
 SPLIT_LAYERS = 2
 
 
