@@ -118,8 +118,9 @@ class MentatBatchGenerator(MentatGenerator):
                                                               [l.seq_id for l in batch])
             self._total_tokens_decoded += len(batch)
             self._update_semantic_vectors(batch, hidden)
-            ahead = self._similarity_ahead(live, batch, logs)
-            self._decide_rows(batch, logits, trees, steps, nacts, logs)
+            launched = self._launch_decisions(batch, logits)
+            ahead = self._similarity_ahead(live, batch, logs)   # queued after the decision record
+            self._decide_rows(batch, logits, trees, steps, nacts, logs, launched)
             self._prune_runs(live, ahead)
             for run in live:
                 if self.step_hook is not None:
@@ -144,8 +145,9 @@ class MentatBatchGenerator(MentatGenerator):
         step, are too young), in the same depth-first order, with unchanged
         vectors and parents. So the mask over the batch's eligible leaves,
         restricted to the survivors, is the mask the prune would compute after
-        the decisions. Its copy completes with the decision record's. Returns
-        None when the rule does not apply (the prune then computes its own)."""
+        the decisions. Its copy is queued after the decision record's, with an
+        event the prune waits for. Returns None when the rule does not apply
+        (the prune then computes its own)."""
         if self.min_steps_before_prune < 1 or self.wrapper.device.type != "cuda":
             return None
         gi_of = {id(run): gi for gi, run in enumerate(runs)}
@@ -155,10 +157,12 @@ class MentatBatchGenerator(MentatGenerator):
                 sv.append(leaf)
                 groups.append(gi_of[id(run)])
         if len(sv) <= 1:
-            return sv, groups, None
+            return sv, groups, None, None
         mask = ops.semantic_similar_mask([l.semantic_vector for l in sv], self._similar_keys(sv), groups,
                                          self.semantic_similarity_threshold, wait=False)
-        return sv, groups, mask
+        ev = torch.cuda.Event()
+        ev.record()
+        return sv, groups, mask, ev
 
     def _prune_runs(self, runs: list, ahead=None) -> None:
         """Every tree's semantic-similarity prune (the rule of _prune_similar, per
@@ -190,7 +194,7 @@ class MentatBatchGenerator(MentatGenerator):
             if pairs:
                 self._apply_prune(run.tree, sv, [(i - base, j - base) for i, j in pairs], run.step, run)
 
-    def _prune_runs_ahead(self, runs: list, sv: list, groups: list, mask) -> None:
+    def _prune_runs_ahead(self, runs: list, sv: list, groups: list, mask, ev) -> None:
         """_prune_runs from the mask of _similarity_ahead (see there)."""
         # Survivors are active leaves of their tree, so two or more of them also
         # satisfy the rule's "more than one active leaf".
@@ -208,6 +212,7 @@ class MentatBatchGenerator(MentatGenerator):
             per[g] = [sv[i] for i in idx]
         if mask is None or not any(per):
             return
+        ev.synchronize()
         ii, jj = np.nonzero(mask.numpy())
         by_group: dict = {}
         for i, j in zip(ii.tolist(), jj.tolist()):

@@ -223,21 +223,36 @@ class MentatGenerator:
         n = len(leaves)
         self._decide_rows(leaves, logits, [tree] * n, [step] * n, [num_active] * n, [self] * n)
 
-    def _decide_rows(self, leaves: list[TreeNode], logits: torch.Tensor, trees: list, steps: list,
-                     num_actives: list, logs: list) -> None:
-        """_decide over a batch whose leaves may belong to different trees: leaf i
-        follows the rules with its own tree's step, frozen num_active, and appends
-        to logs[i].entropy_trace / .branch_points."""
+    def _launch_decisions(self, leaves: list[TreeNode], logits: torch.Tensor):
+        """Queue the step's row kernel and one device-to-host copy of its
+        decision record [H_T, H_pen, K log-probs, K ids (int32 bits carried as
+        float32)]; returns (host record, event after its copy). Work queued
+        later does not delay the record."""
         off, ids = self._penalty_csr(leaves)
         st = ops.row_stats(
             logits.contiguous(), temperature=self.temperature, penalty=self.rep_penalty,
             pen_offsets=off, pen_ids=ids, topk=self.K, pen_stats=True,
         )
-        # One device-to-host copy of the step's decision record
-        # [H_T, H_pen, K log-probs, K ids (int32 bits carried as float32)].
         rec = torch.cat([st.entropy[:, None], st.entropy_pen[:, None], st.topk_lp,
                          st.topk_ids.view(torch.float32)], dim=1)
-        rec_cpu = rec.cpu().numpy()
+        if rec.device.type != "cuda":
+            return rec, None
+        host = torch.empty(rec.shape, dtype=rec.dtype, pin_memory=True)
+        host.copy_(rec, non_blocking=True)
+        ev = torch.cuda.Event()
+        ev.record()
+        return host, ev
+
+    def _decide_rows(self, leaves: list[TreeNode], logits: torch.Tensor, trees: list, steps: list,
+                     num_actives: list, logs: list, launched=None) -> None:
+        """_decide over a batch whose leaves may belong to different trees: leaf i
+        follows the rules with its own tree's step, frozen num_active, and appends
+        to logs[i].entropy_trace / .branch_points. ``launched``: the result of
+        _launch_decisions for these leaves and logits, if already queued."""
+        rec, ev = launched if launched is not None else self._launch_decisions(leaves, logits)
+        if ev is not None:
+            ev.synchronize()
+        rec_cpu = rec.numpy()
         ids_cpu = np.ascontiguousarray(rec_cpu[:, 2 + self.K:2 + 2 * self.K]).view(np.int32)
         # Python lists (the float32 values as Python floats) are far cheaper to
         # index per leaf than numpy scalars.
