@@ -141,6 +141,40 @@ def _line(args, value_gbs: float, ms: float, config: dict, cpu, traffic, extra: 
     return out
 
 
+def _time_graph(step, steps: int, warmup: int, dev):
+    """Untimed warmup on a side stream, then the `steps` calls captured as one
+    graph (as the rollout's decode steps run) and replayed once, untimed, and
+    once between two HIP events on the replay stream."""
+    import torch
+
+    side = torch.cuda.Stream(dev)
+    side.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(side):  # also creates the side stream's workspace before the capture
+        for _ in range(max(warmup, 1)):
+            step()
+    torch.cuda.current_stream(dev).wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        for _ in range(steps):
+            step()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream(dev)
+    graph.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record(stream)
+    graph.replay()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms = e0.elapsed_time(e1) / steps
+    print(f"bench: {steps} steps in one graph replay, mean {ms:.4f} ms, wall {wall:.3f} s", file=sys.stderr,
+          flush=True)
+    return ms
+
+
 def run_decode(args, dev) -> dict:
     import torch
 
@@ -166,7 +200,10 @@ def run_decode(args, dev) -> dict:
         ops.paged_decode(q, ks, vs, layout=b.layout, block_tables=b.block_tables,
                          seq_lens=b.seq_lens, max_seqlen=b.max_seqlen, scale=b.scale, out=out)
 
-    ms = _time_steps(step, args.steps, args.warmup, dev)
+    if args.no_graph:
+        ms = _time_steps(step, args.steps, args.warmup, dev)
+    else:
+        ms = _time_graph(step, args.steps, args.warmup, dev)
     cpu = None
     if not args.no_cpu_baseline:
         print("bench: timing the CPU baseline", file=sys.stderr, flush=True)
@@ -184,6 +221,8 @@ def run_decode(args, dev) -> dict:
         "pool_layout": "native (K [page][kv head][slot][dim], V [page][kv head][dim][slot])",
         "algorithmic_bytes_per_step": nbytes,
         "rotation": "2 copies of Q and the K/V stores used alternately",
+        "launch": "eager, one call per step" if args.no_graph else
+                  "the timed calls captured as one graph and replayed (the rollout's decode steps are graph replays)",
     }
     line = _line(args, nbytes / (ms * 1e-3) / 1e9, ms, config, cpu, _measured_traffic(),
                  {"decode_calls_per_s": round(1e3 / ms, 1)})
@@ -530,6 +569,8 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="minimum host time spent on the CPU baseline")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-graph", action="store_true",
+                    help="decode workload: launch every timed call eagerly instead of replaying them as one graph")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
