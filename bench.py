@@ -257,7 +257,8 @@ def run_tree(args, dev) -> dict:
         state["i"] += 1
         ops.tree_decode(tb.q, ks, vs, block_tables=tb.block_tables, plan=plan, scale=tb.scale, out=out)
 
-    ms = _time_steps(step, args.steps, args.warmup, dev)
+    timer = _time_steps if args.no_graph else _time_graph
+    ms = timer(step, args.steps, args.warmup, dev)
     rows_t = torch.tensor(tb.rows, dtype=torch.int32, device=dev)
 
     def paged():
@@ -266,7 +267,7 @@ def run_tree(args, dev) -> dict:
         ops.paged_decode(tb.q, ks, vs, max_seqlen=max(tb.lens), block_tables=tb.block_tables,
                          seq_lens=tb.seq_lens, seq_rows=rows_t, scale=tb.scale, layout=LAYOUT_NATIVE)
 
-    paged_ms = _time_steps(paged, args.steps, args.warmup, dev)
+    paged_ms = timer(paged, args.steps, args.warmup, dev)
     ub, lb = tb.unique_bytes(), tb.logical_bytes()
     cpu = None
     if not args.no_cpu_baseline:
@@ -280,6 +281,7 @@ def run_tree(args, dev) -> dict:
         "unique_tokens": tb.unique_tokens(), "logical_tokens": tb.logical_tokens(),
         "unique_bytes_per_step": ub, "logical_bytes_per_step": lb,
         "rotation": "4 copies of the K/V stores used in turn",
+        "launch": "eager, one call per step" if args.no_graph else "the timed calls captured as one graph and replayed",
         "plan": {"shared_tasks": plan.n_shared, "solo_items": plan.n_solo, "partial_slots": plan.n_slots,
                  "host_build_ms": round(plan_ms, 2)},
     }
@@ -349,18 +351,16 @@ def run_rows(args, dev) -> dict:
     ent = torch.empty(R, dtype=torch.float32, device=dev)
     gate = torch.empty(R, dtype=torch.uint8, device=dev)
     smp = torch.empty(R, dtype=torch.int32, device=dev)
-    sh = stream_handle(dev)
-
     def step():
         xi = xs[state["i"] % len(xs)]
         st = lib.mentat_row_stats(xi.data_ptr(), xi.stride(0), R, V, 2, T, 1.0, None, None, THR, 0, 1, T, TOP_P,
                                   1234, state["i"], ent.data_ptr(), None, None, gate.data_ptr(), None, None,
-                                  smp.data_ptr(), sh)
+                                  smp.data_ptr(), stream_handle(dev))
         if st != 0:
             raise RuntimeError(f"mentat_row_stats returned {st}")
         state["i"] += 1
 
-    ms = _time_steps(step, args.steps, args.warmup, dev)
+    ms = (_time_steps if args.no_graph else _time_graph)(step, args.steps, args.warmup, dev)
     st = ops.row_stats(x, temperature=T, gate_threshold=THR, sample=True, sample_temperature=T, top_p=TOP_P,
                        seed=1234, step=0, pen_stats=False)
     gated = int(st.gate.sum().item())
