@@ -67,6 +67,7 @@ class MentatBatchGenerator(MentatGenerator):
         self.batch_trace: list[int] = []
         self._total_tokens_decoded = 0
         self._prefill_tokens = 0
+        self._capture_time_s = 0.0
         prefill_s = 0.0
 
         def admit():
@@ -258,11 +259,15 @@ class MentatBatchGenerator(MentatGenerator):
     def get_batch_diagnostics(self) -> dict:
         """Whole-batch metric plus each prompt's traces (the reference's per-prompt keys)."""
         tps = self._total_tokens_decoded / self._decode_time_s if self._decode_time_s > 0 else 0.0
+        with_capture = self._decode_time_s + self._capture_time_s
+        tps_cap = self._total_tokens_decoded / with_capture if with_capture > 0 else 0.0
         kv = self.kv_cache_mgr.get_stats()
         return {
             "decode_tokens_total": self._total_tokens_decoded,
             "decode_time_s": round(self._decode_time_s, 4),
             "decode_throughput_tps": round(tps, 2),
+            "capture_time_s": round(self._capture_time_s, 4),
+            "decode_throughput_tps_incl_capture": round(tps_cap, 2),
             "decode_steps": len(self.batch_trace),
             "max_live_leaves": max(self.batch_trace) if self.batch_trace else 0,
             "prefill_tokens": self._prefill_tokens,

@@ -20,7 +20,9 @@ runs and copied in before the second graph in stream order. Batches are padded t
 the bucket: padding entries carry the token 0 at position 0, read the
 manager's length-0 row (their attention output is zero) and have append plans
 whose destination block is -1, which the append kernel skips; their logits are
-dropped.
+dropped. A bucket's pinned staging is rewritten only after the event recorded
+behind the previous step's copies out of it has completed, so steps queued
+back to back without a host sync never overwrite plans not yet read.
 
 A captured graph holds the addresses of the manager's device tables, of the
 K/V stores, of its own input buffer and of the paged-decode workspace, so
@@ -137,7 +139,8 @@ SPLIT_LAYERS = 2
 
 
 class _Bucket:
-    __slots__ = ("n", "graph", "graph2", "state", "dev", "host", "host_np", "logits", "hidden", "version")
+    __slots__ = ("n", "graph", "graph2", "state", "dev", "host", "host_np", "logits", "hidden", "version",
+                 "copied")
 
 
 class DecodeGraphs:
@@ -331,6 +334,10 @@ class DecodeGraphs:
         self._fill_padding(b.host_np, nb, 0)
         b.dev = torch.empty(size, dtype=torch.int32, device=self.dev)
         b.dev.copy_(b.host)
+        # Recorded after each step's last copy out of b.host: the next step waits
+        # for it before it rewrites the pinned staging.
+        b.copied = torch.cuda.Event()
+        b.copied.record(torch.cuda.current_stream(self.dev))
         s = self._stream
         s.wait_stream(torch.cuda.current_stream(self.dev))
         with torch.cuda.stream(s):
@@ -389,6 +396,10 @@ class DecodeGraphs:
         plan = st["plan"] if overlap else m.plan_append_step_finish(st)   # [L, 7, n]
         m._ensure_pages(int(plan[:max(k, 1) if overlap else L, 4].max()) + 1)
         b = self._get(nb)
+        # The previous step's non-blocking copies read b.host when the stream
+        # reaches them; a caller that queues steps without a host sync could
+        # otherwise overwrite its plans before they are read.
+        b.copied.synchronize()
         h = b.host_np
         plans_h = h[3 * nb:].reshape(L, 7, nb)
         h[0:n] = token_ids
@@ -405,10 +416,12 @@ class DecodeGraphs:
                 raise RuntimeError("DecodeGraphs: a later layer's append needs more table pages than the first")
             plans_h[k:, :, :n] = plan[k:]
             b.dev[cut:].copy_(b.host[cut:], non_blocking=True)
+            b.copied.record()
             b.graph2.replay()
         else:
             plans_h[:, :, :n] = plan
             b.dev.copy_(b.host, non_blocking=True)
+            b.copied.record()
             b.graph.replay()
             if b.graph2 is not None:
                 b.graph2.replay()

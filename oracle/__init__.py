@@ -14,7 +14,9 @@ Modules
               (set-based allocator, fork/free, lazy copy-on-write append)
   sampling    entropy, repetition penalty, gate, argmax/top-K, and the
               Philox4x32-10 temperature/top-p sampler (C, bit-exact spec)
-  tree        PrefixTree ordering and the generator step decisions
+  rollout_cpu the reference's serial rollout on the host (gather + per-sequence
+              SDPA per layer), the CPU baseline of the end-to-end rollout
+  build       compiles csrc/sampling_ref.c into liboracle.so
 
 How each function is pinned (golden vectors, closed forms, library routines,
 invariants) is listed in the module docstrings and exercised by

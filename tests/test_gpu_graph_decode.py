@@ -119,6 +119,52 @@ def test_captured_steps_match_eager_steps(gpu, monkeypatch, split):
     assert all((b.graph2 is not None) == (split < 2) for b in g._graphs.values())
 
 
+@pytest.mark.parametrize("split", [1, 2])
+def test_steps_queued_without_sync_match_eager(gpu, monkeypatch, split):
+    """Captured steps queued back to back with no host synchronisation, behind
+    a GPU kept busy, so each step's host-to-device copies of its plans are still
+    pending when the host plans the next step: every step's logits and the
+    final tables must equal the eager run's (the staging buffer is reused only
+    after the previous step's copies have read it)."""
+    from mentat_amd.core import graph_decode
+
+    monkeypatch.setattr(graph_decode, "SPLIT_LAYERS", split)
+    print(f"case captured steps queued without sync, split={split}", flush=True)
+    model = _bf16_model()
+    we, wg = _wrapper(model, False), _wrapper(model, True)
+    rng = np.random.default_rng(5)
+    steps = 8
+    with torch.no_grad():
+        live = []
+        for p in range(4):
+            ids = torch.tensor([rng.integers(0, 4096, 9 + 6 * p).tolist()], device="cuda")
+            se, sg = we.kv_cache_mgr.allocate_sequence(), wg.kv_cache_mgr.allocate_sequence()
+            we.prefill(ids, se)
+            wg.prefill(ids, sg)
+            live.append(se)
+        toks = rng.integers(0, 4096, (steps, len(live))).tolist()
+        wg.decode_batch_tensor(toks[0], live)          # capture the bucket first
+        ref = [we.decode_batch_tensor(toks[0], live)[0]]
+        ref += [we.decode_batch_tensor(toks[t], live)[0] for t in range(1, steps)]
+        torch.cuda.synchronize()
+        a = torch.randn(4096, 4096, device="cuda")
+        for _ in range(40):                            # ~tens of ms of queued GPU work
+            a = torch.tanh(a @ a)
+        got = [wg.decode_batch_tensor(toks[t], live)[0] for t in range(1, steps)]
+        torch.cuda.synchronize()
+    for t, (lg, le) in enumerate(zip(got, ref[1:]), start=1):
+        scale = float(le.float().abs().max())
+        err = float((lg.float() - le.float()).abs().max())
+        assert err <= 2e-2 * scale + 2e-2, (t, err, scale)
+    me, mg = we.kv_cache_mgr, wg.kv_cache_mgr
+    for layer in range(me.num_layers):
+        for s in live:
+            re_, rg = me._sequences[s].row, mg._sequences[s].row
+            n = len(me._sequences[s].page_table[layer])
+            assert torch.equal(me._tables[layer][re_, :n].cpu(), mg._tables[layer][rg, :n].cpu())
+            assert int(me._lens[layer][re_]) == int(mg._lens[layer][rg])
+
+
 @pytest.mark.parametrize("gate,thr", [("absolute", 2.0)])
 @pytest.mark.parametrize("split", [1, 2])
 def test_rollouts_with_and_without_capture(gpu, monkeypatch, gate, thr, split):
@@ -153,23 +199,26 @@ def test_rollouts_with_and_without_capture(gpu, monkeypatch, gate, thr, split):
             [x[::2] for x in d1["prompts"][p]["branch_points"]]
 
 
-def test_no_garbage_collection_during_capture(gpu):
+@pytest.mark.parametrize("split", [1, 2])
+def test_no_garbage_collection_during_capture(gpu, monkeypatch, split):
     """Captures run with the garbage collector off (collected just before):
     a dropped wrapper's graphs are never torn down inside another capture.
     The forward is spied on; whenever the stream is capturing, gc must be off,
-    and gc's state is restored afterwards."""
+    and gc's state is restored afterwards. split 1 captures each step as two
+    graphs (the layout of models deeper than SPLIT_LAYERS), split 2 as one."""
     import gc
 
     from mentat_amd.core import graph_decode
 
-    print("case gc state during capture", flush=True)
+    print(f"case gc state during capture, split {split}", flush=True)
+    monkeypatch.setattr(graph_decode, "SPLIT_LAYERS", split)
     model = _bf16_model()
     seen = []
     orig = graph_decode.DecodeGraphs._forward
 
-    def spy(self, buf, nb):
+    def spy(self, *args, **kwargs):
         seen.append((torch.cuda.is_current_stream_capturing(), gc.isenabled()))
-        return orig(self, buf, nb)
+        return orig(self, *args, **kwargs)
 
     graph_decode.DecodeGraphs._forward = spy
     try:
@@ -188,6 +237,8 @@ def test_no_garbage_collection_during_capture(gpu):
         graph_decode.DecodeGraphs._forward = orig
     assert any(c for c, _ in seen) and any(not c for c, _ in seen)
     assert all(not on for capturing, on in seen if capturing)
+    # two graphs per bucket capture two forwards per capture
+    assert sum(c for c, _ in seen) == (2 if split == 1 else 1) * 2
     assert gc.isenabled()
 
 
