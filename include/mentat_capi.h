@@ -108,6 +108,25 @@ int mentat_paged_decode(int layout, const void* q, const void* k_cache, const vo
 /* The chunk length (tokens) the reference-layout path uses when chunk_tokens == 0. */
 int mentat_paged_decode_auto_chunk(int N, int Hkv, int block_size, int max_seqlen);
 
+/* mentat_paged_decode without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). It has no counterpart in the reference.
+ * The workspace is a static device array of MENTAT_NOALLOC_SCRATCH_BYTES
+ * inside the library, one per device, held until the process ends; the call
+ * itself allocates nothing. A call whose workspace need
+ * (mentat_paged_decode_workspace_bytes) exceeds that size returns
+ * MENTAT_ESPACE. Every call on a device shares that device's array, so calls
+ * that overlap on one device (other streams or threads) race; calls ordered
+ * on one stream are safe. Results equal mentat_paged_decode's. */
+#define MENTAT_NOALLOC_SCRATCH_BYTES 8388608
+
+int mentat_paged_decode_noalloc(int layout, const void* q, const void* k_cache, const void* v_cache,
+                                const int32_t* block_tables, int64_t table_stride,
+                                const int32_t* seq_rows, const int32_t* seq_lens,
+                                const int32_t* cu_seqlens_k, int64_t num_blocks,
+                                void* out, int N, int Hq, int Hkv, int D, int block_size,
+                                int max_seqlen, float scale, int dtype, int chunk_tokens, void* stream);
+
 /* ------------------------------------------------------------------------
  * Prefix-tree decode attention: the same result as mentat_paged_decode for
  * every query (core/paged_kv_cache.py:289-368 + adapters/attention_backend.py:

@@ -52,6 +52,19 @@ SIGNATURES: dict[str, tuple] = {
             _c_void_p, _c_size, _c_void_p,  # workspace, workspace_bytes, stream
         ],
     ),
+    "mentat_paged_decode_noalloc": (
+        _c_int,
+        [
+            _c_int,  # layout
+            _c_void_p, _c_void_p, _c_void_p,  # q, k_cache, v_cache
+            _c_void_p, _c_i64,  # block_tables, table_stride
+            _c_void_p, _c_void_p,  # seq_rows, seq_lens
+            _c_void_p, _c_i64,  # cu_seqlens_k, num_blocks
+            _c_void_p, _c_int, _c_int, _c_int, _c_int, _c_int,  # out, N, Hq, Hkv, D, block_size
+            _c_int, _c_float, _c_int, _c_int,  # max_seqlen, scale, dtype, chunk_tokens
+            _c_void_p,  # stream
+        ],
+    ),
     "mentat_tree_decode_workspace_bytes": (_c_size, [_c_int] * 4),
     "mentat_tree_decode": (
         _c_int,

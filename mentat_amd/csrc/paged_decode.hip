@@ -22,6 +22,8 @@
 // Split-K: when a launch has more than one chunk per sequence, each unit writes
 // its (m, l, acc) to the workspace and combine_kernel merges them with the usual
 // log-sum-exp rescaling.
+#include <mutex>
+
 #include "mentat_common.h"
 
 namespace mentat {
@@ -348,4 +350,71 @@ extern "C" int mentat_paged_decode(int layout, const void* q, const void* k_cach
     case MENTAT_F32: return paged ? dispatch_d<F32, true>(D, G, p, s) : dispatch_d<F32, false>(D, G, p, s);
     default: return MENTAT_EUNSUP;
   }
+}
+
+// ---- the allocation-free variant ----------------------------------------------------------
+// mentat_paged_decode_noalloc runs mentat_paged_decode with its workspace in this
+// file-scope device array: every device the library runs on holds its own copy
+// (MENTAT_NOALLOC_SCRATCH_BYTES) until the process ends. Its first
+// MENTAT_WORKSPACE_RESERVED bytes are the native path's arrival counters, zeroed
+// once per device by a fill kernel on the first call's stream and left zero by
+// every call; the rest holds a call's partials and is overwritten by the next
+// call. Calls that overlap on one device (other streams, other threads) race
+// on it.
+static __device__ __align__(256) unsigned char scratch[MENTAT_NOALLOC_SCRATCH_BYTES];
+
+namespace mentat {
+
+constexpr int kScratchMaxDevices = 64;
+
+__global__ void zero_words_kernel(uint32_t* p, long n) {
+  for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (long)gridDim.x * blockDim.x) p[i] = 0u;
+}
+
+static std::mutex g_scratch_mu;
+static void* g_scratch_dev[kScratchMaxDevices] = {};
+
+// The device address of the current device's scratch (its host-side name is not
+// a device address). Looked up, and its counters zeroed, once per device.
+static int scratch_address(void** out, hipStream_t stream) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return (int)e;
+  if (dev < 0 || dev >= kScratchMaxDevices) return MENTAT_EUNSUP;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_dev[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return (int)e;
+    if (p == nullptr) return (int)hipErrorInvalidSymbol;
+    const long words = (long)(kWsReserved / sizeof(uint32_t));
+    hipLaunchKernelGGL(zero_words_kernel, dim3((unsigned)((words + 255) / 256)), dim3(256), 0, stream,
+                       (uint32_t*)p, words);
+    e = hipGetLastError();
+    if (e != hipSuccess) return (int)e;
+    g_scratch_dev[dev] = p;
+  }
+  *out = g_scratch_dev[dev];
+  return MENTAT_OK;
+}
+
+}  // namespace mentat
+
+extern "C" int mentat_paged_decode_noalloc(int layout, const void* q, const void* k_cache, const void* v_cache,
+                                           const int32_t* block_tables, int64_t table_stride,
+                                           const int32_t* seq_rows, const int32_t* seq_lens,
+                                           const int32_t* cu_seqlens_k, int64_t num_blocks, void* out, int N,
+                                           int Hq, int Hkv, int D, int block_size, int max_seqlen, float scale,
+                                           int dtype, int chunk_tokens, void* stream) {
+  if (N == 0) return MENTAT_OK;
+  if (N < 0 || Hq <= 0 || Hkv <= 0 || D <= 0 || max_seqlen < 0) return MENTAT_EINVAL;
+  const size_t need = mentat_paged_decode_workspace_bytes(layout, N, Hq, Hkv, D, block_size,
+                                                          max_seqlen > 0 ? max_seqlen : 1, chunk_tokens);
+  if (need > (size_t)MENTAT_NOALLOC_SCRATCH_BYTES) return MENTAT_ESPACE;
+  void* ws = nullptr;
+  const int st = scratch_address(&ws, (hipStream_t)stream);
+  if (st != MENTAT_OK) return st;
+  return mentat_paged_decode(layout, q, k_cache, v_cache, block_tables, table_stride, seq_rows, seq_lens,
+                             cu_seqlens_k, num_blocks, out, N, Hq, Hkv, D, block_size, max_seqlen, scale, dtype,
+                             chunk_tokens, ws, (size_t)MENTAT_NOALLOC_SCRATCH_BYTES, stream);
 }

@@ -37,3 +37,17 @@ def test_abi_version_and_pure_host_queries():
     c = lib.mentat_paged_decode_auto_chunk(64, 8, 16, 4096)
     assert c % 16 == 0 and 16 <= c <= 4096
     assert isinstance(lib.mentat_paged_decode, ctypes._CFuncPtr)
+
+
+def test_noalloc_entry_refuses_sizes_past_its_scratch():
+    """The allocation-free decode checks its workspace need against the static
+    scratch before touching the device (pure host arithmetic on the reference
+    layout: 64 x 32 heads x 4096 chunks of partials are far past 8 MiB)."""
+    lib = _lib.get_lib()
+    need = lib.mentat_paged_decode_workspace_bytes(0, 64, 32, 8, 128, 16, 65536, 16)
+    assert need > 8388608
+    st = lib.mentat_paged_decode_noalloc(0, None, None, None, None, 4096, None, None, None, 65536, None,
+                                         64, 32, 8, 128, 16, 65536, 0.088, 2, 16, None)
+    assert st == _lib.MENTAT_ESPACE
+    assert lib.mentat_paged_decode_noalloc(0, None, None, None, None, 1, None, None, None, 1, None,
+                                           -1, 32, 8, 128, 16, 16, 0.088, 2, 0, None) == _lib.MENTAT_EINVAL
