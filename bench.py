@@ -11,7 +11,11 @@ Prints one JSON line with the whole-job throughput (achieved HBM GB/s of
 algorithmic bytes), the roofline fraction against MI355X's 8 TB/s, and the
 reference's CPU path timed beside it on the same inputs.
 
-Other workloads (their own JSON line, same fields):
+With no --workload (or --workload all) the line also carries "workloads": the
+tree, rows and e2e results below, each with its own ms_per_step, value,
+roofline and cpu_baseline.
+
+Single workloads (their own JSON line, same fields):
   --workload tree   prefix-tree decode at Qwen3-8B attention shapes: 4 trees
                     of 32 leaves over 2048-token prompts (GB/s of unique bytes)
   --workload rows   fused entropy gate + temperature/top-p sampling over
@@ -21,7 +25,7 @@ Other workloads (their own JSON line, same fields):
                     branches per prompt, all prompts continuously batched
                     (branch-decode tokens/s)
 
-  python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload decode|tree|rows]
+  python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload all|decode|tree|rows|e2e|prefill]
 """
 from __future__ import annotations
 
@@ -39,6 +43,7 @@ PEAK_HBM_GBS = 8000.0
 PEAK_BF16_TFLOPS = 2500.0  # dense bf16 MFMA
 TRAFFIC_FILE = os.path.join(HERE, "profiles", "paged_decode_llama3_8b_traffic.txt")
 ROWS_TRAFFIC_FILE = os.path.join(HERE, "profiles", "row_stats_sampling.md")
+TREE_TRAFFIC_FILE = os.path.join(HERE, "profiles", "tree_decode_qwen3_8b.md")
 
 
 def _measured_traffic(path: str = TRAFFIC_FILE):
@@ -49,6 +54,18 @@ def _measured_traffic(path: str = TRAFFIC_FILE):
         return None
     m = re.search(r"^traffic_bytes_per_launch:\s*([0-9.eE+]+)", text, flags=re.M)
     return float(m.group(1)) if m else None
+
+
+def _traffic_source(path: str) -> str | None:
+    """Where roofline.traffic comes from: a committed rocprofv3 --pmc summary (not measured in
+    this run), with the commit and date it was measured at."""
+    try:
+        text = open(path).read()
+    except OSError:
+        return None
+    at = re.search(r"^measured_at:\s*(.+)$", text, flags=re.M)
+    rel = os.path.relpath(path, HERE)
+    return f"committed rocprofv3 --pmc summary {rel}" + (f" ({at.group(1).strip()})" if at else "")
 
 
 def _cpu_baseline(batch, min_seconds: float):
@@ -226,6 +243,7 @@ def run_decode(args, dev) -> dict:
     }
     line = _line(args, nbytes / (ms * 1e-3) / 1e9, ms, config, cpu, _measured_traffic(),
                  {"decode_calls_per_s": round(1e3 / ms, 1)})
+    line["roofline"]["traffic_source"] = _traffic_source(TRAFFIC_FILE)
     line["data"] = "synthetic (seeded N(0,1) Q/K/V, seeded ragged contexts and page permutation)"
     return line
 
@@ -285,11 +303,12 @@ def run_tree(args, dev) -> dict:
         "plan": {"shared_tasks": plan.n_shared, "solo_items": plan.n_solo, "partial_slots": plan.n_slots,
                  "host_build_ms": round(plan_ms, 2)},
     }
-    line = _line(args, ub / (ms * 1e-3) / 1e9, ms, config, cpu, None, {
+    line = _line(args, ub / (ms * 1e-3) / 1e9, ms, config, cpu, _measured_traffic(TREE_TRAFFIC_FILE), {
         "logical_gbs": round(lb / (ms * 1e-3) / 1e9, 1),
         "paged_decode_same_batch_ms": round(paged_ms, 5),
         "speedup_vs_paged_decode": round(paged_ms / ms, 2),
     })
+    line["roofline"]["traffic_source"] = _traffic_source(TREE_TRAFFIC_FILE)
     line["data"] = "synthetic (seeded trees grown through the paged cache manager; RMS-normed N(0,1) q/k, N(0,1) v)"
     return line
 
@@ -354,8 +373,8 @@ def run_rows(args, dev) -> dict:
     def step():
         xi = xs[state["i"] % len(xs)]
         st = lib.mentat_row_stats(xi.data_ptr(), xi.stride(0), R, V, 2, T, 1.0, None, None, THR, 0, 1, T, TOP_P,
-                                  1234, state["i"], ent.data_ptr(), None, None, gate.data_ptr(), None, None,
-                                  smp.data_ptr(), stream_handle(dev))
+                                  1234, state["i"], ent.data_ptr(), None, None, None, gate.data_ptr(), None,
+                                  None, smp.data_ptr(), stream_handle(dev))
         if st != 0:
             raise RuntimeError(f"mentat_row_stats returned {st}")
         state["i"] += 1
@@ -390,6 +409,7 @@ def run_rows(args, dev) -> dict:
     }
     line = _line(args, nbytes / (ms * 1e-3) / 1e9, ms, config, cpu, _measured_traffic(ROWS_TRAFFIC_FILE),
                  {"rows_per_s": round(R * 1e3 / ms, 1)})
+    line["roofline"]["traffic_source"] = _traffic_source(ROWS_TRAFFIC_FILE)
     line["data"] = "synthetic (seeded N(0, sigma_r) logits)"
     return line
 
@@ -550,7 +570,12 @@ def run_e2e(args, dev) -> dict:
     if not args.no_cpu_baseline:
         cpu = _cpu_baseline_e2e(model, prompts[0], new_tokens, knobs, args.cpu_seconds)
     line = _line(args, 0.0, ms, config, cpu, None)
-    line.update({"metric": METRIC, "value": round(d["decode_throughput_tps"], 1), "unit": "tokens/s"})
+    line.update({"metric": METRIC, "value": round(d["decode_throughput_tps"], 1), "unit": "tokens/s",
+                 "steps": steps, "warmup": 1,
+                 # graph capture of the decode buckets runs before the decode timer (the reference has
+                 # no such phase): its seconds, and the rate with them counted as decode time
+                 "capture_s": d["capture_time_s"],
+                 "tokens_per_s_incl_capture": d["decode_throughput_tps_incl_capture"]})
     # per-step HBM floor: the weights once per step
     line["roofline"] = {"bound": "hbm", "achieved": round(wbytes / (ms * 1e-3) / 1e9, 1), "peak": PEAK_HBM_GBS,
                         "unit": "GB/s", "frac": round(wbytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
@@ -559,12 +584,46 @@ def run_e2e(args, dev) -> dict:
     return line
 
 
+def _summary(line: dict) -> dict:
+    """The fields of a workload's line that its nested entry keeps."""
+    keep = ("value", "unit", "ms_per_step", "steps", "warmup", "dtype", "config", "roofline", "cpu_baseline")
+    out = {k: line[k] for k in keep if k in line}
+    for k, v in line.items():
+        if k not in out and k not in ("metric", "n_gpus", "higher_is_better", "scaling", "vs_baseline", "data"):
+            out[k] = v
+    return out
+
+
+def run_all(args, dev) -> dict:
+    """The headline (paged decode at Llama-3-8B shapes) with the other measured
+    workloads nested under "workloads": prefix-tree decode, the fused entropy
+    gate + sampling step and the end-to-end rollout (branch-decode tokens/s).
+    A workload that fails is reported with its error instead of its numbers."""
+    import torch
+
+    line = run_decode(args, dev)
+    nested = {}
+    for name, fn in (("tree", run_tree), ("rows", run_rows), ("e2e", run_e2e)):
+        torch.cuda.empty_cache()
+        t0 = time.perf_counter()
+        try:
+            nested[name] = _summary(fn(args, dev))
+        except Exception as exc:  # reported, not hidden: the headline still prints
+            nested[name] = {"error": f"{type(exc).__name__}: {exc}"}
+            print(f"bench: workload {name} failed: {exc!r}", file=sys.stderr, flush=True)
+        nested[name]["wall_s"] = round(time.perf_counter() - t0, 1)
+        torch.cuda.synchronize()
+    line["workloads"] = nested
+    return line
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--workload", choices=("decode", "tree", "rows", "e2e", "prefill"), default="decode")
+    ap.add_argument("--workload", choices=("all", "decode", "tree", "rows", "e2e", "prefill"), default="all",
+                    help="all (default): the paged-decode headline plus tree, rows and e2e nested in one line")
     ap.add_argument("--e2e-new-tokens", type=int, default=512)
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="minimum host time spent on the CPU baseline")
@@ -584,7 +643,7 @@ def main() -> int:
 
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
-    run = {"decode": run_decode, "tree": run_tree, "rows": run_rows, "e2e": run_e2e,
+    run = {"all": run_all, "decode": run_decode, "tree": run_tree, "rows": run_rows, "e2e": run_e2e,
            "prefill": run_prefill}[args.workload]
     print(json.dumps(run(args, dev)), flush=True)
     return 0

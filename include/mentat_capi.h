@@ -293,12 +293,18 @@ int mentat_table_copy_rows(int32_t* tables, int32_t* seq_lens, int L, int64_t ro
  * elements apart), one workgroup per row, all outputs device arrays:
  *   out_entropy[R]      entropy (nats) of softmax(x / temperature), raw logits
  *                       (compute_entropy at the gate temperature,
- *                       core/generator_utils.py:196-202, core/generator.py:342)
+ *                       core/generator_utils.py:196-202, core/generator.py:342),
+ *                       rounded as torch's device kernels round it in the logits
+ *                       dtype: y = rnd(x * fl(1/T)), p = rnd(e/s), lp = rnd(fl(y-m) - ln s),
+ *                       t = rnd(p*lp) (NaN -> 0), H = -rnd(sum t), e = exp2(fl(y-m)*log2 e)
+ *   out_entropy_f32[R]  the same entropy with fp32 arithmetic and no dtype rounding
+ *                       (the reference's value for fp32 logits; may be NULL)
  *   out_gate[R]         out_entropy > gate_threshold (may be NULL)
  *   xp                  repetition penalty over the row's ids in CSR
  *                       pen_offsets[R+1] / pen_ids (duplicates ignored; NULL or
  *                       penalty == 1: none), core/generator_utils.py:205-230
- *   out_entropy_pen[R]  entropy of softmax(xp) (core/generator.py:293; may be NULL)
+ *   out_entropy_pen[R]  entropy of softmax(xp) (core/generator.py:293; may be NULL),
+ *                       rounded as out_entropy (T = 1)
  *   out_lse[R]          log-sum-exp of xp (may be NULL)
  *   out_topk[R,topk], out_topk_lp[R,topk]
  *                       the topk (0..8) best log_softmax(xp) values in the logits
@@ -316,7 +322,8 @@ int mentat_row_stats(const void* logits, int64_t row_stride, int R, int V, int d
                      float penalty, const int32_t* pen_offsets, const int32_t* pen_ids,
                      float gate_threshold, int topk, int do_sample, float sample_temperature,
                      float top_p, uint64_t seed, uint64_t step, float* out_entropy,
-                     float* out_entropy_pen, float* out_lse, uint8_t* out_gate, int32_t* out_topk,
+                     float* out_entropy_f32, float* out_entropy_pen, float* out_lse, uint8_t* out_gate,
+                     int32_t* out_topk,
                      float* out_topk_lp, int32_t* out_sample, void* stream);
 
 /* Philox4x32-10 blocks: out[4i..4i+3] = rounds(counters[4i..], keys[2i..]) for

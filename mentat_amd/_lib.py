@@ -144,7 +144,7 @@ SIGNATURES: dict[str, tuple] = {
             _c_float, _c_void_p, _c_void_p,  # penalty, pen_offsets, pen_ids
             _c_float, _c_int, _c_int, _c_float,  # gate_threshold, topk, do_sample, sample_temperature
             _c_float, _c_u64, _c_u64,  # top_p, seed, step
-            _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,  # outputs
+            _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,  # outputs
             _c_void_p,  # stream
         ],
     ),

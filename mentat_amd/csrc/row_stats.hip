@@ -12,7 +12,13 @@
 // Per row (reference semantics, cited):
 //   H_T      entropy of softmax(x / T) of the raw logits, in nats
 //            (compute_entropy at the gate temperature, core/generator_utils.py:196-202,
-//            called at core/generator.py:342); fp32 instead of the logits dtype.
+//            called at core/generator.py:342), with the rounding chain torch's device
+//            kernels give it in the logits dtype: y = rnd(x * fl(1/T)) (division by a
+//            scalar is a multiply by its reciprocal), m = max y, e = exp2(fl(y - m) *
+//            log2(e)), s = sum e, p = rnd(e / s), lp = rnd((y - m) - log s),
+//            t = rnd(p * lp), H = -rnd(sum t); rnd rounds to the logits dtype (identity
+//            for f32). Both sums are formed in double from fp32 terms and rounded to
+//            float once (torch sums in float in its own order).
 //   gate     H_T > gate_threshold (absolute gate; the relative EMA gate of
 //            core/generator.py:346-369 is applied by the host on H_T).
 //   xp       repetition penalty on the row's generated ids (deduplicated, as the
@@ -43,7 +49,7 @@ struct RowParams {
   const void* logits;
   int64_t row_stride;  // elements
   int R, V;
-  float ent_c;         // log2(e) / T for the gate entropy
+  float inv_t;         // fl(1 / T): the gate entropy's y = rnd(x * inv_t)
   float samp_c;        // log2(e) / T for the sampler
   float penalty;       // 1.0 = off
   const int32_t* pen_offsets;  // [R+1] or null
@@ -55,6 +61,7 @@ struct RowParams {
   int do_sample;
   float gate_threshold;
   float* out_entropy;      // [R]
+  float* out_entropy_f32;  // [R] or null: H_T with fp32 arithmetic throughout (no dtype rounding)
   float* out_entropy_pen;  // [R] or null
   float* out_lse;          // [R] or null (log-sum-exp of xp)
   uint8_t* out_gate;       // [R] or null
@@ -157,7 +164,7 @@ constexpr int kHistBins = 4096;  // widest radix level: 12 key bits
 template <int NW>
 struct RowSharedT {
   static constexpr int kWaves = NW;
-  float f[NW * 4];
+  alignas(8) float f[NW * 8];  // also four doubles per wave
   uint64_t u[NW];
   uint64_t hist0[kHistBins];  // first radix level (shared by both selections)
   uint64_t hist1[kHistBins];  // deeper levels
@@ -173,6 +180,71 @@ struct RowSharedT {
 };
 using RowShared = RowSharedT<kRowWaves>;
 
+// ---- wave-wide sums, minima and prefix sums through DPP (register moves, no LDS round trip) ----
+constexpr int kDppRowShr1 = 0x111, kDppRowShr2 = 0x112, kDppRowShr3 = 0x113, kDppRowShr4 = 0x114,
+              kDppRowShr8 = 0x118, kDppRowBcast15 = 0x142, kDppRowBcast31 = 0x143;
+// Lanes whose row / bank is masked off, or that have no source lane, read 0.
+template <int CTRL, int RM = 0xF, int BM = 0xF>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, RM, BM, true);
+}
+template <int CTRL, int RM = 0xF, int BM = 0xF>
+__device__ __forceinline__ uint64_t dpp_u64(uint64_t v) {
+  return ((uint64_t)dpp_u32<CTRL, RM, BM>((uint32_t)(v >> 32)) << 32) | dpp_u32<CTRL, RM, BM>((uint32_t)v);
+}
+template <int CTRL>
+__device__ __forceinline__ double dpp_f64(double v) {
+  return __builtin_bit_cast(double, dpp_u64<CTRL>(__builtin_bit_cast(uint64_t, v)));
+}
+// Butterflies within each row of 16 lanes: every lane then holds its row's total.
+template <typename T, class MOVE>
+__device__ __forceinline__ T row_total(T v, MOVE mv) {
+  v += mv(v, std::integral_constant<int, kDppQuadXor1>{});
+  v += mv(v, std::integral_constant<int, kDppQuadXor2>{});
+  v += mv(v, std::integral_constant<int, kDppRowHalfMirror>{});
+  v += mv(v, std::integral_constant<int, kDppRowMirror>{});
+  return v;
+}
+__device__ __forceinline__ uint32_t rl32(uint32_t v, int l) { return (uint32_t)__builtin_amdgcn_readlane((int)v, l); }
+__device__ __forceinline__ uint64_t rl64(uint64_t v, int l) {
+  return ((uint64_t)rl32((uint32_t)(v >> 32), l) << 32) | rl32((uint32_t)v, l);
+}
+// Wave totals (wave-uniform), the four row totals added in row order.
+__device__ __forceinline__ uint32_t wave_sum_u32(uint32_t v) {
+  v = row_total(v, [](uint32_t x, auto c) { return dpp_u32<decltype(c)::value>(x); });
+  return rl32(v, 0) + rl32(v, 16) + rl32(v, 32) + rl32(v, 48);
+}
+__device__ __forceinline__ uint64_t wave_sum_u64(uint64_t v) {
+  v = row_total(v, [](uint64_t x, auto c) { return dpp_u64<decltype(c)::value>(x); });
+  return rl64(v, 0) + rl64(v, 16) + rl64(v, 32) + rl64(v, 48);
+}
+__device__ __forceinline__ double wave_sum_f64(double v) {
+  v = row_total(v, [](double x, auto c) { return dpp_f64<decltype(c)::value>(x); });
+  const uint64_t u = __builtin_bit_cast(uint64_t, v);
+  return ((__builtin_bit_cast(double, rl64(u, 0)) + __builtin_bit_cast(double, rl64(u, 16))) +
+          __builtin_bit_cast(double, rl64(u, 32))) + __builtin_bit_cast(double, rl64(u, 48));
+}
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
+  v = min(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, kDppQuadXor1, 0xF, 0xF, false));
+  v = min(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, kDppQuadXor2, 0xF, 0xF, false));
+  v = min(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, kDppRowHalfMirror, 0xF, 0xF, false));
+  v = min(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, kDppRowMirror, 0xF, 0xF, false));
+  return min(min(rl32(v, 0), rl32(v, 16)), min(rl32(v, 32), rl32(v, 48)));
+}
+// Inclusive prefix sum over the wave's lanes (lane order): window sums within rows, then the
+// row totals carried across rows by row broadcasts.
+__device__ __forceinline__ uint64_t wave_incl_scan_u64(uint64_t v) {
+  const uint64_t v0 = v;
+  v += dpp_u64<kDppRowShr1>(v0);
+  v += dpp_u64<kDppRowShr2>(v0);
+  v += dpp_u64<kDppRowShr3>(v0);
+  v += dpp_u64<kDppRowShr4, 0xF, 0xE>(v);
+  v += dpp_u64<kDppRowShr8, 0xF, 0xC>(v);
+  v += dpp_u64<kDppRowBcast15, 0xA, 0xF>(v);
+  v += dpp_u64<kDppRowBcast31, 0xC, 0xF>(v);
+  return v;
+}
+
 __device__ __forceinline__ float wave_max(float v) {
 _Pragma("clang loop unroll(full)")
   for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
@@ -181,14 +253,6 @@ _Pragma("clang loop unroll(full)")
 __device__ __forceinline__ float wave_sum(float v) {
 _Pragma("clang loop unroll(full)")
   for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
-  return v;
-}
-__device__ __forceinline__ uint64_t wave_sum_u64(uint64_t v) {
-_Pragma("clang loop unroll(full)")
-  for (int o = 32; o >= 1; o >>= 1) {
-    const uint32_t lo = __shfl_xor((uint32_t)v, o), hi = __shfl_xor((uint32_t)(v >> 32), o);
-    v += ((uint64_t)hi << 32) | lo;
-  }
   return v;
 }
 
@@ -232,12 +296,7 @@ __device__ __forceinline__ uint64_t shfl_up_u64(uint64_t v, int o) {
 template <class SH>
 __device__ __forceinline__ uint64_t block_excl_scan_u64(uint64_t v, uint64_t& total, SH& sh) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  uint64_t inc = v;
-_Pragma("clang loop unroll(full)")
-  for (int o = 1; o < 64; o <<= 1) {
-    const uint64_t t = shfl_up_u64(inc, o);
-    if (lane >= o) inc += t;
-  }
+  const uint64_t inc = wave_incl_scan_u64(v);
   __syncthreads();
   if (lane == 63) sh.u[wave] = inc;
   __syncthreads();
@@ -250,6 +309,55 @@ _Pragma("clang loop unroll(full)")
   total = tot;
   return base + inc - v;
 }
+
+// Sum of up to 4 doubles over the block (every thread gets the totals).
+template <int NVAL, class SH>
+__device__ __forceinline__ void block_sum_f64(double (&v)[NVAL], SH& sh) {
+  static_assert(NVAL <= 4, "four doubles per wave slot");
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+_Pragma("clang loop unroll(full)")
+  for (int i = 0; i < NVAL; ++i) v[i] = wave_sum_f64(v[i]);
+  __syncthreads();
+  if (lane == 0) {
+_Pragma("clang loop unroll(full)")
+    for (int i = 0; i < NVAL; ++i) reinterpret_cast<double*>(sh.f)[wave * 4 + i] = v[i];
+  }
+  __syncthreads();
+_Pragma("clang loop unroll(full)")
+  for (int i = 0; i < NVAL; ++i) {
+    double a = 0.0;
+    for (int w = 0; w < SH::kWaves; ++w) a += reinterpret_cast<const double*>(sh.f)[w * 4 + i];
+    v[i] = a;
+  }
+}
+
+// ---- the entropy chain in the logits dtype (compute_entropy, core/generator_utils.py:196-202,
+// and log_softmax, core/generator.py:283/308, as torch's device kernels round them) --------------
+// A row's softmax state: its max m (a value of the dtype), s = fl(sum exp2(fl(y - m) * log2 e))
+// and ln s. Keys (log-probs) are rnd(fl(y - m) - ln s).
+struct ChainState {
+  float m, s, logs;
+};
+__device__ __forceinline__ ChainState chain_state(float m, double s) {
+  const float sf = (float)s;
+  return ChainState{m, sf, logf(sf)};
+}
+__device__ __forceinline__ float chain_exp(float y, float m) { return exp2f((y - m) * kLog2e); }
+// t = rnd(rnd(e / s) * rnd(fl(y - m) - ln s)) for one token of value y.
+template <class RE>
+__device__ __forceinline__ float chain_term(float y, const ChainState& c) {
+  const float d = y - c.m;
+  const float pr = RE::round(__fdiv_rn(exp2f(d * kLog2e), c.s));
+  const float lp = RE::round(d - c.logs);
+  const float t = RE::round(pr * lp);
+  return t != t ? 0.f : t;  // torch.nan_to_num(nan=0.0): 0 * -inf for a -inf logit
+}
+// H = -rnd(sum t) from the double sum of the terms.
+template <class RE>
+__device__ __forceinline__ float chain_entropy(double S) { return -RE::round((float)S); }
+// The entropy with fp32 arithmetic throughout (y = x * fl(1/T) unrounded, exact sums):
+// H = ln s - (sum e * d) / s with d = fl(y - m), e = exp2(d * log2 e).
+__device__ __forceinline__ float f32_entropy(double s, double sed) { return (float)(log(s) - sed / s); }
 
 // (key, idx) ordering for top-K: larger key first, then lower index.
 __device__ __forceinline__ bool tk_better(float ka, int ia, float kb, int ib) {
@@ -389,32 +497,34 @@ __device__ __forceinline__ void rows_generic(const RowParams& p, const int row, 
   { const int op[2] = {0, 0}; block_reduce<2>(mx, op, sh); }
   const float m_raw = mx[0], m_pen = mx[1];
 
-  // ---- pass 2: entropy sums (base 2); with sampling, the first radix level of
-  // the fixed-point masses (a histogram by the top 12 key bits) ----
-  // The T = 1 sums of xp feed the top-K keys, the log-sum-exp and H_pen only.
+  // ---- pass 2: the softmax denominators in double (the gate chain on y = rnd(x * inv_t), the
+  // T = 1 chain on xp); with sampling, the first radix level of the fixed-point masses (a
+  // histogram by the top 12 key bits) ----
+  // The T = 1 chain of xp feeds the top-K keys, the log-sum-exp and H_pen only.
   const bool need_pen_sums = p.topk > 0 || p.out_entropy_pen != nullptr || p.out_lse != nullptr;
   constexpr int L0 = RE::level_bits[0];
   if (p.do_sample) {
     for (int t = tid; t < (1 << L0); t += kRowThreads) sh.hist0[t] = 0;
     __syncthreads();
   }
-  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  const float m_t = RE::round(m_raw * p.inv_t);  // rounding keeps the order: the largest y
+  const float m_32 = m_raw * p.inv_t;
+  const bool want_f32 = p.out_entropy_f32 != nullptr;
+  double den[4] = {0.0, 0.0, 0.0, 0.0};
   ROW_FOR_GROUPS(
     const int i0 = (c * kRowThreads + tid) * EPV;
     static_for<EPV>([&](auto ec_) __attribute__((always_inline)) {
       constexpr int e = decltype(ec_)::value;
       if (i0 + e >= p.V) return;
-      const float y = (x[e] - m_raw) * p.ent_c;
-      const float ey = fast_exp2(y);
-      acc[0] += ey;
-      acc[1] += ey > 0.f ? ey * y : 0.f;
-      const float xp = penal(i0 + e, x[e]);
-      if (need_pen_sums) {
-        const float y1 = (xp - m_pen) * kLog2e;
-        const float e1 = fast_exp2(y1);
-        acc[2] += e1;
-        acc[3] += e1 > 0.f ? e1 * y1 : 0.f;
+      den[0] += (double)chain_exp(RE::round(x[e] * p.inv_t), m_t);
+      if (want_f32) {
+        const float d32 = x[e] * p.inv_t - m_32;
+        const float e32 = exp2f(d32 * kLog2e);
+        den[2] += (double)e32;
+        den[3] += e32 > 0.f ? (double)e32 * (double)d32 : 0.0;
       }
+      const float xp = penal(i0 + e, x[e]);
+      if (need_pen_sums) den[1] += (double)chain_exp(xp, m_pen);
       if (p.do_sample) {
         // q = floor(det_exp2(ys) * 2^40) is exactly 0 for ys < -41
         const float ys = (xp - m_pen) * p.samp_c;
@@ -425,13 +535,28 @@ __device__ __forceinline__ void rows_generic(const RowParams& p, const int row, 
       }
         });
     )
-  { const int op[4] = {1, 1, 1, 1}; block_reduce<4>(acc, op, sh); }
-  const float H_T = (log2f(acc[0]) - acc[1] / acc[0]) * kLn2;
-  const float H_pen = (log2f(acc[2]) - acc[3] / acc[2]) * kLn2;
-  const float logsum = logf(acc[2]);  // ln(sum exp(xp - max)), as log_softmax forms it
+  block_sum_f64<4>(den, sh);
+  const ChainState c_t = chain_state(m_t, den[0]), c_1 = chain_state(m_pen, den[1]);
+  if (want_f32 && tid == 0) p.out_entropy_f32[row] = f32_entropy(den[2], den[3]);
+  // ---- pass 2b: the entropy terms t of both chains ----
+  double ent[2] = {0.0, 0.0};
+  const bool want_hpen = p.out_entropy_pen != nullptr;
+  ROW_FOR_GROUPS(
+    const int i0 = (c * kRowThreads + tid) * EPV;
+    static_for<EPV>([&](auto ec_) __attribute__((always_inline)) {
+      constexpr int e = decltype(ec_)::value;
+      if (i0 + e >= p.V) return;
+      ent[0] += (double)chain_term<RE>(RE::round(x[e] * p.inv_t), c_t);
+      if (want_hpen) ent[1] += (double)chain_term<RE>(penal(i0 + e, x[e]), c_1);
+        });
+    )
+  block_sum_f64<2>(ent, sh);
+  const float H_T = chain_entropy<RE>(ent[0]);
+  const float H_pen = chain_entropy<RE>(ent[1]);
+  const float logsum = c_1.logs;  // ln(sum exp(xp - max)), as log_softmax forms it
   if (tid == 0) {
     p.out_entropy[row] = H_T;
-    if (p.out_entropy_pen) p.out_entropy_pen[row] = H_pen;  // NaN-free only when computed
+    if (p.out_entropy_pen) p.out_entropy_pen[row] = H_pen;
     if (p.out_lse) p.out_lse[row] = m_pen + logsum;
     if (p.out_gate) p.out_gate[row] = H_T > p.gate_threshold ? 1 : 0;
   }
@@ -749,9 +874,10 @@ template <> struct Bits16<F16> {
 __host__ __device__ constexpr uint32_t key16(uint32_t raw) { return raw ^ ((raw & 0x8000u) ? 0xffffu : 0x8000u); }
 __device__ __forceinline__ uint32_t raw16_of_key(uint32_t k) { return k ^ ((k & 0x8000u) ? 0x8000u : 0xffffu); }
 
-constexpr int kFT = 1024;                                      // threads per row
+constexpr int kFT = 512;                                       // threads per row (2 waves per SIMD:
+                                                               // 256 VGPRs each, room for the row)
 constexpr int kFW = kFT / 64;
-constexpr int kFastChunks = 20;                                // chunks of kFT 16-byte groups
+constexpr int kFastChunks = 40;                                // chunks of kFT 16-byte groups
 constexpr int kFastMaxV = kFastChunks * kFT * 8;               // 163,840 (the penalty bits' LDS)
 constexpr int kFastPenWords = kFastMaxV / 32;
 constexpr int kHistWords = 32768;                              // 65,536 16-bit counts
@@ -763,7 +889,7 @@ struct FastShared {
   static constexpr int kWaves = kFW;
   uint64_t slab_mass[kSlabs];  // sampler mass per slab of 256 values
   uint32_t slab_cnt[kSlabs];   // tokens per slab
-  float f[kFW * 4];
+  alignas(8) float f[kFW * 8];  // also four doubles per wave
   uint64_t u[kFW];
   uint32_t g[kFW * 4];
   uint32_t sel[8];     // one slot per resolution step
@@ -780,19 +906,20 @@ __device__ __forceinline__ uint64_t shfl_down_u64(uint64_t v, int o) {
   const uint32_t lo = __shfl_down((uint32_t)v, o), hi = __shfl_down((uint32_t)(v >> 32), o);
   return ((uint64_t)hi << 32) | lo;
 }
-__device__ __forceinline__ uint32_t wave_sum_u32(uint32_t v) {
-_Pragma("clang loop unroll(full)")
-  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
-  return v;
-}
-__device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
-_Pragma("clang loop unroll(full)")
-  for (int o = 32; o >= 1; o >>= 1) v = min(v, (uint32_t)__shfl_xor(v, o));
-  return v;
+
+// The row's registers: 32-dword vectors of 8 groups each. A group is read back with a
+// wave-uniform index (GPR indexing), so the passes over the row are compact loops rather
+// than one unrolled copy of their body per group.
+typedef uint32_t u32x32 __attribute__((ext_vector_type(32)));
+__device__ __forceinline__ uint4 row_group(const u32x32& v, int g) {
+  const int b = __builtin_amdgcn_readfirstlane(g) * 4;
+  return make_uint4(v[b], v[b + 1], v[b + 2], v[b + 3]);
 }
 
-// Rows must start on 16-byte boundaries (16-byte buffer loads).
-template <typename T>
+// Rows must start on 16-byte boundaries (16-byte buffer loads). NG: 16-byte groups per thread
+// (V <= NG * kFT * 8, NG a multiple of 8); the whole row stays in registers (NG * 4 VGPRs), so
+// it is read from HBM once.
+template <typename T, int NG>
 __global__ __launch_bounds__(kFT) void row_stats_fast_kernel(RowParams p) {
   constexpr bool AL = true;
   using RE = RowElem<T>;
@@ -808,6 +935,9 @@ __global__ __launch_bounds__(kFT) void row_stats_fast_kernel(RowParams p) {
   __shared__ uint32_t pbits[kFastPenWords];
   __shared__ FastShared fs;
   static_assert(sizeof(RowSharedT<kFW>) <= sizeof(hist), "the multi-pass path reuses the histogram's LDS");
+  static_assert(NG <= kFastChunks, "the penalty bits cover kFastChunks groups per thread");
+  static_assert(NG % 8 == 0, "groups are held 8 to a 32-dword vector");
+  constexpr int NV = NG / 8;
   const int V = p.V;
   const char* rp = (const char*)p.logits + (long)row * p.row_stride * (long)sizeof(S);
   const int nchunks = (V + kFT * EPV - 1) / (kFT * EPV);
@@ -824,6 +954,19 @@ __global__ __launch_bounds__(kFT) void row_stats_fast_kernel(RowParams p) {
   auto nkey = [](float v) __attribute__((always_inline)) -> uint32_t { return key16(B16::raw(v == 0.f ? 0.f : v)); };
   auto kval = [](uint32_t k) __attribute__((always_inline)) -> float { return B16::val(raw16_of_key(k)); };
 
+  // ---- pass A: the whole row into registers, every load in flight at once (bytes past the row
+  // read as zero); each group is counted into the 65,536-value histogram as it lands, with the
+  // largest and smallest keys on the way ----
+  u32x32 d[NV];
+  static_for<NG>([&](auto c_) __attribute__((always_inline)) {
+    constexpr int c = decltype(c_)::value;
+    const uint4 w = load_raw(c);
+    d[c / 8][(c % 8) * 4] = w.x;
+    d[c / 8][(c % 8) * 4 + 1] = w.y;
+    d[c / 8][(c % 8) * 4 + 2] = w.z;
+    d[c / 8][(c % 8) * 4 + 3] = w.w;
+    __builtin_amdgcn_sched_barrier(0);  // issue in chunk order: groups land in order and are counted so
+  });
   const bool use_pen = p.penalty != 1.0f && p.pen_offsets != nullptr;
   const int nwords = (V + 31) / 32;
   {
@@ -835,7 +978,6 @@ __global__ __launch_bounds__(kFT) void row_stats_fast_kernel(RowParams p) {
     fs.top_pen = 0;
     fs.bad = 0;
   }
-  __syncthreads();
   // The draw's uniform depends only on (seed, row, step).
   uint64_t U = 0;
   if (p.do_sample) {
@@ -843,45 +985,43 @@ __global__ __launch_bounds__(kFT) void row_stats_fast_kernel(RowParams p) {
     philox4x32_10(c4, (uint32_t)p.seed, (uint32_t)(p.seed >> 32));
     U = ((uint64_t)c4[0] << 32) | c4[1];
   }
-
-  // ---- pass A: count the raw values (kRowUnroll 16-byte loads in flight per thread); the
-  // largest and smallest keys on the way ----
+  __syncthreads();
   auto count1 = [&](uint32_t k) __attribute__((always_inline)) { atomicAdd(&hist[k >> 1], 1u << ((k & 1u) << 4)); };
   uint32_t kmx = 0, kmn = 0xffffffffu;
-  for (int c0 = 0; c0 < nchunks; c0 += kRowUnroll) {
-    uint4 w[kRowUnroll];
+  // (each vector's loop waits only for its own 8 loads: counting overlaps the later ones)
+  static_for<NV>([&](auto v_) __attribute__((always_inline)) {
+    constexpr int v = decltype(v_)::value;
+#pragma clang loop unroll(disable)
+    for (int g = 0; g < 8; ++g) {
+    const int c = v * 8 + g;
+    if (c >= nchunks) break;
+    const int i0 = (c * kFT + tid) * EPV;
+    const uint4 w = row_group(d[v], g);
+    const uint32_t dw[4] = {w.x, w.y, w.z, w.w};
+    if (i0 + EPV <= V) {
 _Pragma("clang loop unroll(full)")
-    for (int u = 0; u < kRowUnroll; ++u) w[u] = load_raw(c0 + u);  // zeros past the row
+      for (int k = 0; k < 4; ++k) {
+        // both halves' keys at once: xor 0xffff into a negative half, 0x8000 into a positive one
+        const uint32_t k2 = dw[k] ^ ((((dw[k] >> 15) & 0x10001u) * 0x7fffu) | 0x80008000u);
+        const uint32_t lo = k2 & 0xffffu, hi = k2 >> 16;
+        count1(lo);
+        count1(hi);
+        kmx = max(kmx, max(lo, hi));
+        kmn = min(kmn, min(lo, hi));
+      }
+    } else {
 _Pragma("clang loop unroll(full)")
-    for (int u = 0; u < kRowUnroll; ++u) {
-      const int c = c0 + u;
-      const int i0 = (c * kFT + tid) * EPV;
-      const uint32_t dw[4] = {w[u].x, w[u].y, w[u].z, w[u].w};
-      if (c >= nchunks) {
-      } else if (i0 + EPV <= V) {
-_Pragma("clang loop unroll(full)")
-        for (int k = 0; k < 4; ++k) {
-          // both halves' keys at once: xor 0xffff into a negative half, 0x8000 into a positive one
-          const uint32_t k2 = dw[k] ^ ((((dw[k] >> 15) & 0x10001u) * 0x7fffu) | 0x80008000u);
-          const uint32_t lo = k2 & 0xffffu, hi = k2 >> 16;
-          count1(lo);
-          count1(hi);
-          kmx = max(kmx, max(lo, hi));
-          kmn = min(kmn, min(lo, hi));
-        }
-      } else {
-_Pragma("clang loop unroll(full)")
-        for (int e = 0; e < EPV; ++e) {
-          if (i0 + e < V) {
-            const uint32_t k = key16((dw[e >> 1] >> ((e & 1) * 16)) & 0xffffu);
-            count1(k);
-            kmx = max(kmx, k);
-            kmn = min(kmn, k);
-          }
+      for (int e = 0; e < EPV; ++e) {
+        if (i0 + e < V) {
+          const uint32_t k = key16((dw[e >> 1] >> ((e & 1) * 16)) & 0xffffu);
+          count1(k);
+          kmx = max(kmx, k);
+          kmn = min(kmn, k);
         }
       }
     }
-  }
+    }
+  });
 _Pragma("clang loop unroll(full)")
   for (int o = 32; o >= 1; o >>= 1) {
     kmx = max(kmx, (uint32_t)__shfl_xor(kmx, o));
@@ -911,29 +1051,106 @@ _Pragma("clang loop unroll(full)")
   uint32_t top = top_raw;
   bool ok = top_raw < kInfKey && kmn > kNegInfKey;  // non-finite rows take the multi-pass path
   const float m_raw = kval(top_raw);
-  float H_T = 0.f;
-  if (ok && use_pen) {
-    // Entropy of the raw values, then every penalised token (each distinct id once: the one
-    // that clears its bit) moves to its penalised value; the bits are set again for pass B.
-    float a2[2] = {0.f, 0.f};
-    for (int i = 0; i < kHistWords / kFT; ++i) {
-      const int w = tid + i * kFT;
-      const uint32_t wd = hist[w];
-      if (!wd) continue;
+  const float m_t = RE::round(m_raw * p.inv_t);  // the largest y = rnd(x * inv_t)
+
+  // ---- sweeps over the histogram (wave w takes slabs w, w + 16, ...; lane l the four values
+  // 4l .. 4l + 3 of the slab) ----
+  const bool need_pen_sums = p.topk > 0 || p.out_entropy_pen != nullptr || p.out_lse != nullptr;
+  const bool want_hpen = p.out_entropy_pen != nullptr;
+  const bool want_mass = p.do_sample != 0;
+  // The softmax denominators (in double; slab token counts into fs.slab_cnt, the token total
+  // into fs.total): the gate chain of the raw values (do_t) and the T = 1 chain (do_1).
+  // With do_32, also the fp32 entropy's sums of the raw values (den[2], den[3]).
+  const float m_32 = m_raw * p.inv_t;
+  auto sweep_den = [&](bool do_t, bool do_1, bool do_32, bool masses, float m_1, double (&den)[4]) __attribute__((always_inline)) {
+    const uint2* h2 = reinterpret_cast<const uint2*>(hist);
+    uint32_t total = 0;
+    den[0] = 0.0;
+    den[1] = 0.0;
+    den[2] = 0.0;
+    den[3] = 0.0;
+    uint2 nxt = h2[wave * (kSlabBins / 4) + lane];
+    for (int i = 0; i < kSlabs / kFW; ++i) {
+      const int s = wave + i * kFW;
+      const uint2 wd = nxt;
+      if (i + 1 < kSlabs / kFW) nxt = h2[(s + kFW) * (kSlabBins / 4) + lane];  // next slab's read in flight
+      uint64_t mass = 0;
+      uint32_t cnt = 0;
+      if (__any((wd.x | wd.y) != 0u)) {
+        if ((wd.x | wd.y) != 0u) {
 _Pragma("clang loop unroll(full)")
-      for (int h = 0; h < 2; ++h) {
-        const uint32_t n = (wd >> (16 * h)) & 0xffffu;
-        if (!n) continue;
-        const float y = (kval((uint32_t)(2 * w + h)) - m_raw) * p.ent_c;
-        const float e = fast_exp2(y);
-        a2[0] += (float)n * e;
-        a2[1] += e > 0.f ? (float)n * (e * y) : 0.f;
+          for (int b = 0; b < 4; ++b) {
+            const uint32_t n = ((b < 2 ? wd.x : wd.y) >> ((b & 1) * 16)) & 0xffffu;
+            if (!n) continue;
+            const float v = kval((uint32_t)(s * kSlabBins + lane * 4 + b));
+            const double dn = (double)n;
+            if (do_t) den[0] += dn * (double)chain_exp(RE::round(v * p.inv_t), m_t);
+            if (do_1) den[1] += dn * (double)chain_exp(v, m_1);
+            if (do_32) {
+              const float d32 = v * p.inv_t - m_32;
+              const float e32 = exp2f(d32 * kLog2e);
+              den[2] += dn * (double)e32;
+              if (e32 > 0.f) den[3] += dn * ((double)e32 * (double)d32);
+            }
+            if (masses) {
+              const float ys = (v - m_1) * p.samp_c;
+              if (ys >= -41.0f) mass += (uint64_t)n * det_q(ys);
+            }
+            cnt += n;
+          }
+        }
+        total += cnt;
+        if (masses) mass = wave_sum_u64(mass);
+        cnt = wave_sum_u32(cnt);
+      }
+      if (lane == 0) {
+        fs.slab_mass[s] = mass;
+        fs.slab_cnt[s] = cnt;
       }
     }
-    { const int op[2] = {1, 1}; block_reduce<2>(a2, op, fs); }
-    H_T = (log2f(a2[0]) - a2[1] / a2[0]) * kLn2;
+    total = wave_sum_u32(total);
+    if (lane == 0) atomicAdd(&fs.total, total);
+    block_sum_f64<4>(den, fs);
+  };
+  // The entropy terms of both chains over the slabs holding tokens (fs.slab_cnt of the last
+  // sweep_den on this histogram).
+  auto sweep_ent = [&](bool do_t, bool do_1, const ChainState& ct, const ChainState& c1, double (&ent)[2]) __attribute__((always_inline)) {
+    const uint2* h2 = reinterpret_cast<const uint2*>(hist);
+    ent[0] = 0.0;
+    ent[1] = 0.0;
+    for (int i = 0; i < kSlabs / kFW; ++i) {
+      const int s = wave + i * kFW;
+      if (fs.slab_cnt[s] == 0) continue;
+      const uint2 wd = h2[s * (kSlabBins / 4) + lane];
+_Pragma("clang loop unroll(full)")
+      for (int b = 0; b < 4; ++b) {
+        const uint32_t n = ((b < 2 ? wd.x : wd.y) >> ((b & 1) * 16)) & 0xffffu;
+        if (!n) continue;
+        const float v = kval((uint32_t)(s * kSlabBins + lane * 4 + b));
+        const double dn = (double)n;
+        if (do_t) ent[0] += dn * (double)chain_term<RE>(RE::round(v * p.inv_t), ct);
+        if (do_1) ent[1] += dn * (double)chain_term<RE>(v, c1);
+      }
+    }
+    block_sum_f64<2>(ent, fs);
+  };
+
+  const bool want_f32 = p.out_entropy_f32 != nullptr;
+  float H_T = 0.f, H32 = 0.f;
+  ChainState c_t{m_t, 0.f, 0.f};
+  if (ok && use_pen) {
+    // The gate entropy of the raw values, then every penalised token (each distinct id once: the
+    // one that clears its bit) moves to its penalised value; the bits are set again for pass B.
+    double den[4], ent[2];
+    sweep_den(true, false, want_f32, false, m_raw, den);
+    c_t = chain_state(m_t, den[0]);
+    H32 = f32_entropy(den[2], den[3]);
+    __syncthreads();
+    sweep_ent(true, false, c_t, c_t, ent);
+    H_T = chain_entropy<RE>(ent[0]);
     // (the id list is read only now: its loads would otherwise wait for the row's)
     for (int w = tid; w < nwords; w += kFT) pbits[w] = 0u;
+    if (tid == 0) fs.total = 0;
     __syncthreads();
     const int b = p.pen_offsets[row], e = p.pen_offsets[row + 1];
     for (int j = b + tid; j < e; j += kFT) {
@@ -986,78 +1203,36 @@ _Pragma("clang loop unroll(full)")
   }
   const float m_pen = kval(top);
 
-  // ---- resolution: one sweep over the slabs (wave w takes slabs w, w + 16, ...; lane l the
-  // four values 4l .. 4l + 3 of the slab) for the entropy sums, each slab's mass and count, and
-  // the token total (a 16-bit count that overflowed leaves it short of V) ----
-  const bool need_pen_sums = p.topk > 0 || p.out_entropy_pen != nullptr || p.out_lse != nullptr;
-  const bool want_mass = p.do_sample != 0, want_cnt = p.topk > 0;
-  auto unit_mass = [&](uint32_t k) __attribute__((always_inline)) -> uint64_t {
-    const float ys = (kval(k) - m_pen) * p.samp_c;
-    return ys >= -41.0f ? det_q(ys) : 0;
-  };
-  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  // ---- resolution: each slab's mass and count, the denominators and the token total (a 16-bit
+  // count that overflowed leaves it short of V), then the entropy terms ----
+  ChainState c_1{m_pen, 0.f, 0.f};
   if (ok) {
-    const uint2* h2 = reinterpret_cast<const uint2*>(hist);
-    uint32_t total = 0;
-    uint2 nxt = h2[wave * (kSlabBins / 4) + lane];
-    for (int i = 0; i < kSlabs / kFW; ++i) {
-      const int s = wave + i * kFW;
-      const uint2 wd = nxt;
-      if (i + 1 < kSlabs / kFW) nxt = h2[(s + kFW) * (kSlabBins / 4) + lane];  // next slab's read in flight
-      uint64_t mass = 0;
-      uint32_t cnt = 0;
-      if (__any((wd.x | wd.y) != 0u)) {
-        if ((wd.x | wd.y) != 0u) {
-_Pragma("clang loop unroll(full)")
-          for (int b = 0; b < 4; ++b) {
-            const uint32_t n = ((b < 2 ? wd.x : wd.y) >> ((b & 1) * 16)) & 0xffffu;
-            if (!n) continue;
-            const uint32_t k = (uint32_t)(s * kSlabBins + lane * 4 + b);
-            const float v = kval(k), fn = (float)n;
-            if (!use_pen) {
-              const float y = (v - m_raw) * p.ent_c;
-              const float e = fast_exp2(y);
-              acc[0] += fn * e;
-              acc[1] += e > 0.f ? fn * (e * y) : 0.f;
-            }
-            if (need_pen_sums) {
-              const float y1 = (v - m_pen) * kLog2e;
-              const float e1 = fast_exp2(y1);
-              acc[2] += fn * e1;
-              acc[3] += e1 > 0.f ? fn * (e1 * y1) : 0.f;
-            }
-            if (want_mass) {
-              const float ys = (v - m_pen) * p.samp_c;
-              if (ys >= -41.0f) mass += (uint64_t)n * det_q(ys);
-            }
-            cnt += n;
-          }
-        }
-        total += cnt;
-        if (want_mass) mass = wave_sum_u64(mass);
-        if (want_cnt) cnt = wave_sum_u32(cnt);
+    double den[4];
+    sweep_den(!use_pen, need_pen_sums, want_f32 && !use_pen, want_mass, m_pen, den);
+    ok = fs.total == (uint32_t)V;
+    if (ok) {
+      if (!use_pen) {
+        c_t = chain_state(m_t, den[0]);
+        H32 = f32_entropy(den[2], den[3]);
       }
-      if (lane == 0) {
-        fs.slab_mass[s] = mass;
-        fs.slab_cnt[s] = cnt;
+      c_1 = chain_state(m_pen, den[1]);
+      if (!use_pen || want_hpen) {
+        double ent[2];
+        sweep_ent(!use_pen, want_hpen, c_t, c_1, ent);
+        if (!use_pen) H_T = chain_entropy<RE>(ent[0]);
+        if (want_hpen && tid == 0) p.out_entropy_pen[row] = chain_entropy<RE>(ent[1]);
       }
     }
-    total = wave_sum_u32(total);
-    if (lane == 0) atomicAdd(&fs.total, total);
-    { const int op[4] = {1, 1, 1, 1}; block_reduce<4>(acc, op, fs); }
-    ok = fs.total == (uint32_t)V;
   }
   if (!ok) {
     __syncthreads();
     rows_generic<T, AL, kFT>(p, row, *reinterpret_cast<RowSharedT<kFW>*>(hist), pbits);
     return;
   }
-  if (!use_pen) H_T = (log2f(acc[0]) - acc[1] / acc[0]) * kLn2;
-  const float H_pen = (log2f(acc[2]) - acc[3] / acc[2]) * kLn2;
-  const float logsum = logf(acc[2]);
+  const float logsum = c_1.logs;
   if (tid == 0) {
     p.out_entropy[row] = H_T;
-    if (p.out_entropy_pen) p.out_entropy_pen[row] = H_pen;
+    if (want_f32) p.out_entropy_f32[row] = H32;
     if (p.out_lse) p.out_lse[row] = m_pen + logsum;
     if (p.out_gate) p.out_gate[row] = H_T > p.gate_threshold ? 1 : 0;
   }
@@ -1065,6 +1240,10 @@ _Pragma("clang loop unroll(full)")
 
   // Wave-level resolution (no barriers): the slab, then the value, holding position pos, keys
   // descending. Lane l holds slabs kSlabs-1-4l .. kSlabs-4-4l (largest keys in lane 0).
+  auto unit_mass = [&](uint32_t k) __attribute__((always_inline)) -> uint64_t {
+    const float ys = (kval(k) - m_pen) * p.samp_c;
+    return ys >= -41.0f ? det_q(ys) : 0;
+  };
   auto rd64 = [](uint64_t v, int l) __attribute__((always_inline)) -> uint64_t {
     return ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(v >> 32), l) << 32) |
            (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, l);
@@ -1092,12 +1271,9 @@ _Pragma("clang loop unroll(full)")
       m[b] = n == 0 ? 0 : by_mass ? (uint64_t)n * unit_mass(k) : (uint64_t)n;
       tot += m[b];
     }
-    uint64_t inc = tot;  // suffix sum: lanes above hold larger keys
-_Pragma("clang loop unroll(full)")
-    for (int o = 1; o < 64; o <<= 1) {
-      const uint64_t t = shfl_down_u64(inc, o);
-      if (lane + o < 64) inc += t;
-    }
+    // suffix sum (lanes above hold larger keys): the wave total less the exclusive prefix
+    const uint64_t pre = wave_incl_scan_u64(tot);
+    const uint64_t inc = rl64(pre, 63) - pre + tot;
     uint64_t run = above + (inc - tot), a = 0;
     uint32_t key = 0;
     bool hit = false;
@@ -1123,13 +1299,7 @@ _Pragma("clang loop unroll(full)")
       sm[q] = src64 ? src64[s] : (uint64_t)src32[s];
       lt += sm[q];
     }
-    uint64_t inc = lt;
-_Pragma("clang loop unroll(full)")
-    for (int o = 1; o < 64; o <<= 1) {
-      const uint64_t t = shfl_up_u64(inc, o);
-      if (lane >= o) inc += t;
-    }
-    return inc - lt;
+    return wave_incl_scan_u64(lt) - lt;
   };
 
   // ---- the draw (wave 0): nucleus boundary, kept mass, r, the drawn value and its tie index ----
@@ -1184,61 +1354,87 @@ _Pragma("clang loop unroll(full)")
   const uint32_t j_r = p.do_sample ? fs.sel[1] : 0u;
   const float v_thr = p.topk > 0 ? kval(fs.sel[2] & 0xffffu) : __builtin_huge_valf();
 
-  // ---- pass B (the row again): each lane's 8-bit mask of tokens equal to the drawn value per
-  // chunk, and the top-K candidates ----
-  uint8_t* masks = reinterpret_cast<uint8_t*>(hist);         // [kFastChunks][kFW][64 lanes]
+  // ---- pass B (the row from registers): how many of each lane's 8 tokens of every chunk equal
+  // the drawn value, and the top-K candidates. The drawn value is matched on the raw bits of a
+  // dword's two values at once (a half of dw ^ (raw_r * 0x10001) is zero iff that value is the
+  // drawn one; -0 is the drawn zero too). A group holds a candidate only if its largest key
+  // reaches the threshold's. Penalised tokens, the row's last partial group and candidate groups
+  // (all rare) are checked element by element on their values ----
+  uint8_t* counts = reinterpret_cast<uint8_t*>(hist);        // [kFastChunks][kFW][64 lanes]
   uint2* cand = reinterpret_cast<uint2*>(hist + 8192);       // [kCandCap] (log-prob bits, index)
   const float v_match = p.do_sample ? v_r : __builtin_nanf("");  // NaN matches nothing
+  const uint32_t raw_r = raw16_of_key(fs.sel[0] & 0xffffu);
+  const uint32_t raw_r2 = raw_r * 0x10001u;
+  const bool r_zero = raw_r == 0u;                             // -0 (raw 0x8000) matches as well
+  const uint32_t key_thr = p.topk > 0 ? fs.sel[2] & 0xffffu : 0x10000u;  // above every key: no candidates
+  const uint32_t key_thr_any = key_thr == 0x8000u ? 0x7fffu : key_thr;  // -0 reaches a +0 threshold
+  // bit 15 / bit 31 set where the low / high half of x is zero (no carry crosses the halves)
+  auto zero_halves = [](uint32_t x) __attribute__((always_inline)) -> uint32_t {
+    return ~(((x & 0x7fff7fffu) + 0x7fff7fffu) | x) & 0x80008000u;
+  };
   __syncthreads();
-  if (tid == 0) fs.ncand = 0;
-  __syncthreads();
-  for (int c0 = 0; c0 < nchunks; c0 += kRowUnroll) {
-    uint4 w[kRowUnroll];
-_Pragma("clang loop unroll(full)")
-    for (int u = 0; u < kRowUnroll; ++u) w[u] = load_raw(c0 + u);
-_Pragma("clang loop unroll(full)")
-    for (int u = 0; u < kRowUnroll; ++u) {
-      const int c = c0 + u;
-      if (c >= nchunks) continue;
-      const int i0 = (c * kFT + tid) * EPV;
-      const uint4 d = w[u];
-      const uint32_t vm = i0 + EPV <= V ? 0xffu : i0 >= V ? 0u : (1u << (V - i0)) - 1u;  // valid elements
-      const uint32_t pb = (use_pen && i0 < V) ? (pbits[i0 >> 5] >> (i0 & 31)) & vm & 0xffu : 0u;
-      const uint32_t plain = vm & ~pb;
-      uint32_t mt = 0, cm = 0;
-_Pragma("clang loop unroll(full)")
-      for (int e = 0; e < EPV; ++e) {
-        const float xv = RE::get(d, e);
-        const bool pl = ((plain >> e) & 1u) != 0;
-        mt |= (pl && xv == v_match) ? 1u << e : 0u;
-        cm |= (pl && xv >= v_thr) ? 1u << e : 0u;
-      }
-      // penalised elements and top-K candidates (both rare), one at a time
-      for (uint32_t bits = pb | cm; bits != 0u; bits &= bits - 1u) {
-        const int e = __builtin_ctz(bits);
-        float xv = RE::get(d, e);
-        if ((pb >> e) & 1u) {
-          xv = pen_value(xv);
-          if (xv == v_match) mt |= 1u << e;
-          if (!(xv >= v_thr)) continue;
-        }
-        if (p.topk > 0) {
-          const uint32_t pos = atomicAdd(&fs.ncand, 1u);
-          if (pos < kCandCap)
-            cand[pos] = make_uint2(__float_as_uint(RE::round((xv - m_pen) - logsum)), (uint32_t)(i0 + e));
-        }
-      }
-      if (p.do_sample) masks[(c * kFW + wave) * 64 + lane] = (uint8_t)mt;
-    }
+  if (tid == 0) {
+    fs.ncand = 0;
+    fs.sel[3] = 0xffffffffu;
   }
+  __syncthreads();
+  static_for<NV>([&](auto v_) __attribute__((always_inline)) {
+    constexpr int v = decltype(v_)::value;
+#pragma clang loop unroll(disable)
+    for (int g = 0; g < 8; ++g) {
+    const int c = v * 8 + g;
+    if (c >= nchunks) break;
+    const int i0 = (c * kFT + tid) * EPV;
+    const uint4 dd = row_group(d[v], g);
+    const uint32_t vm = i0 + EPV <= V ? 0xffu : i0 >= V ? 0u : (1u << (V - i0)) - 1u;  // valid elements
+    const uint32_t pb = (use_pen && i0 < V) ? (pbits[i0 >> 5] >> (i0 & 31)) & vm & 0xffu : 0u;
+    const bool exact = vm != 0xffu || pb != 0u;
+    uint32_t nm = 0;
+    if (p.do_sample && !exact) {
+      uint32_t f0 = zero_halves(dd.x ^ raw_r2), f1 = zero_halves(dd.y ^ raw_r2);
+      uint32_t f2 = zero_halves(dd.z ^ raw_r2), f3 = zero_halves(dd.w ^ raw_r2);
+      if (r_zero) {
+        f0 |= zero_halves(dd.x ^ 0x80008000u);
+        f1 |= zero_halves(dd.y ^ 0x80008000u);
+        f2 |= zero_halves(dd.z ^ 0x80008000u);
+        f3 |= zero_halves(dd.w ^ 0x80008000u);
+      }
+      nm = __builtin_popcount(f0) + __builtin_popcount(f1) + __builtin_popcount(f2) + __builtin_popcount(f3);
+    }
+    uint32_t cm = 0;
+    if (p.topk > 0) {
+      const uint32_t dw[4] = {dd.x, dd.y, dd.z, dd.w};
+      uint32_t kmax = 0;
+_Pragma("clang loop unroll(full)")
+      for (int k = 0; k < 4; ++k) {
+        const uint32_t k2 = dw[k] ^ ((((dw[k] >> 15) & 0x10001u) * 0x7fffu) | 0x80008000u);
+        kmax = max(kmax, max(k2 & 0xffffu, k2 >> 16));
+      }
+      cm = kmax >= key_thr_any ? vm : 0u;
+    }
+    // element by element: candidate groups, penalised tokens, the last partial group
+    for (uint32_t bits = cm | (exact ? vm : 0u); bits != 0u; bits &= bits - 1u) {
+      const int e = __builtin_ctz(bits);
+      float xv = RE::get(dd, e);
+      if ((pb >> e) & 1u) xv = pen_value(xv);
+      if (exact && xv == v_match) ++nm;
+      if (p.topk > 0 && xv >= v_thr) {
+        const uint32_t pos = atomicAdd(&fs.ncand, 1u);
+        if (pos < kCandCap)
+          cand[pos] = make_uint2(__float_as_uint(RE::round((xv - m_pen) - logsum)), (uint32_t)(i0 + e));
+      }
+    }
+    if (p.do_sample) counts[(c * kFW + wave) * 64 + lane] = (uint8_t)nm;
+    }
+  });
   __syncthreads();
 
   if (p.topk > 0) {
     auto block_best = [&](float& bk, int& bi) __attribute__((always_inline)) {
       for (int o = 32; o >= 1; o >>= 1) {
-        const float ok = __shfl_xor(bk, o);
+        const float ok2 = __shfl_xor(bk, o);
         const int oi = __shfl_xor(bi, o);
-        if (tk_better(ok, oi, bk, bi)) { bk = ok; bi = oi; }
+        if (tk_better(ok2, oi, bk, bi)) { bk = ok2; bi = oi; }
       }
       __syncthreads();
       if (lane == 0) { fs.bk[wave] = bk; fs.bi[wave] = bi; }
@@ -1268,7 +1464,8 @@ _Pragma("clang loop unroll(full)")
         if (ci == bi) { ck = kNegInf; ci = 0x7fffffff; }
       }
     } else {
-      // more tied candidates than LDS holds: K selections over the row, read again
+      // more tied candidates than LDS holds: K selections over the row, read again (rare:
+      // the registers are not used here, so the selections add no register pressure)
       float prev_k = __builtin_huge_valf();
       int prev_i = -1;
       for (int j = 0; j < p.topk; ++j) {
@@ -1301,50 +1498,66 @@ _Pragma("clang loop unroll(full)")
     }
   }
 
-  // ---- the drawn token: the j_r-th (by index) token of value v_r. Thread t takes the masks of
-  // (chunk t / 16, wave t % 16), whose tokens follow in index order (lane, then element) ----
+  // ---- the drawn token: the j_r-th (by index) token of value v_r. Thread t takes the counts of
+  // (chunk t / kFW, wave t % kFW), whose tokens follow in index order (lane, then element); the
+  // one whose range holds j_r names the lane and the rank within its 8 tokens, and that lane finds
+  // the token in its registers ----
   if (p.do_sample) {
     const int t = tid;
-    uint4 mw[4] = {};
-    uint32_t v = 0;
+    uint4 cw[4] = {};
+    uint32_t n = 0;
     if (t < nchunks * kFW) {
 _Pragma("clang loop unroll(full)")
       for (int q = 0; q < 4; ++q) {
-        mw[q] = reinterpret_cast<const uint4*>(masks + t * 64)[q];
-        v += __builtin_popcount(mw[q].x) + __builtin_popcount(mw[q].y) + __builtin_popcount(mw[q].z) +
-             __builtin_popcount(mw[q].w);
+        cw[q] = reinterpret_cast<const uint4*>(counts + t * 64)[q];
+        // counts are at most 8: the bytes of a word sum without carries
+        n += ((cw[q].x * 0x01010101u) >> 24) + ((cw[q].y * 0x01010101u) >> 24) + ((cw[q].z * 0x01010101u) >> 24) +
+             ((cw[q].w * 0x01010101u) >> 24);
       }
     }
     uint64_t tot;
-    const uint64_t ex = block_excl_scan_u64((uint64_t)v, tot, fs);
-    if (v && ex <= j_r && j_r < ex + v) {
-      // the 16 words of lane masks (4 lanes each): popcounts, then the word, byte and bit
-      // holding match j_r (static selections: no dynamic register indexing)
-      const uint32_t wv[16] = {mw[0].x, mw[0].y, mw[0].z, mw[0].w, mw[1].x, mw[1].y, mw[1].z, mw[1].w,
-                               mw[2].x, mw[2].y, mw[2].z, mw[2].w, mw[3].x, mw[3].y, mw[3].z, mw[3].w};
-      uint32_t seen = (uint32_t)ex, wsel = 0, base = 0;
-      int wi_found = -1;
-      static_for<16>([&](auto wi_) __attribute__((always_inline)) {
-        constexpr int wi = decltype(wi_)::value;
-        const uint32_t n = (uint32_t)__builtin_popcount(wv[wi]);
-        if (wi_found < 0 && seen + n > j_r) { wi_found = wi; wsel = wv[wi]; base = seen; }
-        seen += n;
+    const uint64_t ex = block_excl_scan_u64((uint64_t)n, tot, fs);
+    if (n && ex <= j_r && j_r < ex + n) {
+      const uint32_t wv[16] = {cw[0].x, cw[0].y, cw[0].z, cw[0].w, cw[1].x, cw[1].y, cw[1].z, cw[1].w,
+                               cw[2].x, cw[2].y, cw[2].z, cw[2].w, cw[3].x, cw[3].y, cw[3].z, cw[3].w};
+      uint32_t seen = (uint32_t)ex;
+      int lane_found = -1;
+      uint32_t rank = 0;
+      static_for<64>([&](auto l_) __attribute__((always_inline)) {
+        constexpr int l = decltype(l_)::value;
+        const uint32_t k = (wv[l / 4] >> (8 * (l % 4))) & 0xffu;
+        if (lane_found < 0 && seen + k > j_r) { lane_found = l; rank = j_r - seen; }
+        seen += k;
       });
-      int found = -1;
-      if (wi_found >= 0) {
-        static_for<4>([&](auto bb_) __attribute__((always_inline)) {
-          constexpr int bb = decltype(bb_)::value;
-          uint32_t mb = (wsel >> (8 * bb)) & 0xffu;
-          const uint32_t n = (uint32_t)__builtin_popcount(mb);
-          if (found < 0 && base + n > j_r) {
-            for (uint32_t r = j_r - base; r > 0; --r) mb &= mb - 1u;  // drop the earlier matches
-            found = (wi_found * 4 + bb) * EPV + __builtin_ctz(mb);      // lane * 8 + element
+      fs.sel[3] = (uint32_t)t;
+      fs.sel[4] = (uint32_t)lane_found;
+      fs.sel[5] = rank;
+    }
+    __syncthreads();
+    const uint32_t owner = fs.sel[3];
+    if (owner != 0xffffffffu && wave == (int)(owner % kFW)) {
+      const int c = (int)(owner / kFW), lf = (int)fs.sel[4];
+      const uint32_t rank = fs.sel[5];
+      static_for<NV>([&](auto v_) __attribute__((always_inline)) {
+        constexpr int v = decltype(v_)::value;
+        if (v != c / 8) return;
+        const uint4 dd = row_group(d[v], c % 8);
+        if (lane != lf) return;
+        const int i0 = (c * kFT + tid) * EPV;
+        const uint32_t pb = (use_pen && i0 < V) ? (pbits[i0 >> 5] >> (i0 & 31)) & 0xffu : 0u;
+        uint32_t seen = 0;
+        int found = -1;
+        static_for<EPV>([&](auto e_) __attribute__((always_inline)) {
+          constexpr int e = decltype(e_)::value;
+          float xv = RE::get(dd, e);
+          if ((pb >> e) & 1u) xv = pen_value(xv);
+          if (i0 + e < V && xv == v_match) {
+            if (found < 0 && seen == rank) found = i0 + e;
+            ++seen;
           }
-          base += n;
         });
-      }
-      if (found >= 0 && p.out_sample)
-        p.out_sample[row] = ((t / kFW) * kFT + (t % kFW) * 64) * EPV + found;
+        if (found >= 0 && p.out_sample) p.out_sample[row] = found;
+      });
     }
   }
 }
@@ -1368,7 +1581,14 @@ static int dispatch_rows(const RowParams& p, hipStream_t s) {
   const bool aligned = (((uintptr_t)p.logits) & 15u) == 0 && ((p.row_stride * (long)sizeof(S)) & 15) == 0;
   if constexpr (sizeof(S) == 2) {
     if (aligned && p.V <= kFastMaxV) {
-      hipLaunchKernelGGL((row_stats_fast_kernel<T>), dim3(p.R), dim3(kFT), 0, s, p);
+      // the smallest register-resident instantiation that holds the row
+      const long groups = ((long)p.V + kFT * 8 - 1) / (kFT * 8);
+      if (groups <= 16)
+        hipLaunchKernelGGL((row_stats_fast_kernel<T, 16>), dim3(p.R), dim3(kFT), 0, s, p);
+      else if (groups <= 32)
+        hipLaunchKernelGGL((row_stats_fast_kernel<T, 32>), dim3(p.R), dim3(kFT), 0, s, p);
+      else
+        hipLaunchKernelGGL((row_stats_fast_kernel<T, kFastChunks>), dim3(p.R), dim3(kFT), 0, s, p);
       return (int)hipGetLastError();
     }
   }
@@ -1387,7 +1607,7 @@ extern "C" int mentat_row_stats(const void* logits, int64_t row_stride, int R, i
                                 float temperature, float penalty, const int32_t* pen_offsets,
                                 const int32_t* pen_ids, float gate_threshold, int topk, int do_sample,
                                 float sample_temperature, float top_p, uint64_t seed, uint64_t step,
-                                float* out_entropy, float* out_entropy_pen, float* out_lse,
+                                float* out_entropy, float* out_entropy_f32, float* out_entropy_pen, float* out_lse,
                                 uint8_t* out_gate, int32_t* out_topk, float* out_topk_lp,
                                 int32_t* out_sample, void* stream) {
   if (R == 0) return MENTAT_OK;
@@ -1398,13 +1618,14 @@ extern "C" int mentat_row_stats(const void* logits, int64_t row_stride, int R, i
   if (R > 2147483647 / 2) return MENTAT_EINVAL;
   RowParams p;
   p.logits = logits; p.row_stride = row_stride; p.R = R; p.V = V;
-  p.ent_c = (float)(1.4426950408889634 / (double)temperature);
+  p.inv_t = 1.0f / temperature;
   p.samp_c = do_sample ? (float)(1.4426950408889634 / (double)sample_temperature) : 0.f;
   p.penalty = penalty; p.pen_offsets = pen_offsets; p.pen_ids = pen_ids;
   p.topk = topk;
   p.top_p_q32 = (uint64_t)llrint((double)top_p * 4294967296.0);
   p.seed = seed; p.step = step; p.do_sample = do_sample; p.gate_threshold = gate_threshold;
-  p.out_entropy = out_entropy; p.out_entropy_pen = out_entropy_pen; p.out_lse = out_lse;
+  p.out_entropy = out_entropy; p.out_entropy_f32 = out_entropy_f32; p.out_entropy_pen = out_entropy_pen;
+  p.out_lse = out_lse;
   p.out_gate = out_gate; p.out_topk = out_topk; p.out_topk_lp = out_topk_lp; p.out_sample = out_sample;
   hipStream_t s = (hipStream_t)stream;
   switch (dtype) {

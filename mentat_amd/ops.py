@@ -471,7 +471,8 @@ def table_copy_rows(tables: torch.Tensor, seq_lens: Optional[torch.Tensor], src_
 
 @dataclass
 class RowStats:
-    entropy: torch.Tensor                 # [R] f32, entropy of softmax(x / T)
+    entropy: torch.Tensor                 # [R] f32, entropy of softmax(x / T), rounded as torch in the dtype
+    entropy_f32: Optional[torch.Tensor]   # [R] f32, the same with fp32 arithmetic (no dtype rounding)
     gate: torch.Tensor                    # [R] u8, entropy > gate_threshold
     entropy_pen: Optional[torch.Tensor]   # [R] f32, entropy of softmax(xp)
     lse: Optional[torch.Tensor]           # [R] f32, log-sum-exp of xp
@@ -495,12 +496,15 @@ def row_stats(
     seed: int = 0,
     step: int = 0,
     pen_stats: Optional[bool] = None,
+    entropy_f32: bool = False,
 ) -> RowStats:
     """Fused per-row entropy, gate, repetition penalty, top-K and top-p draw
     (mentat_row_stats in include/mentat_capi.h) over logits [R, V].
 
     ``pen_stats`` (default: ``topk > 0``) also returns the entropy and
     log-sum-exp of the penalised row (``entropy_pen``, ``lse``; None otherwise).
+    ``entropy`` is rounded as the reference's compute_entropy is in the logits
+    dtype; ``entropy_f32=True`` also returns it computed in fp32 throughout.
     """
     if pen_stats is None:
         pen_stats = topk > 0
@@ -522,6 +526,7 @@ def row_stats(
     f32 = dict(dtype=torch.float32, device=dev)
     out = RowStats(
         entropy=torch.empty(R, **f32),
+        entropy_f32=torch.empty(R, **f32) if entropy_f32 else None,
         gate=torch.empty(R, dtype=torch.uint8, device=dev),
         entropy_pen=torch.empty(R, **f32) if pen_stats else None,
         lse=torch.empty(R, **f32) if pen_stats else None,
@@ -536,7 +541,7 @@ def row_stats(
         float(penalty), ptr(pen_offsets), ptr(pen_ids),
         float(gate_threshold), int(topk), int(bool(sample)), float(sample_temperature),
         float(top_p), int(seed) & (2**64 - 1), int(step) & (2**64 - 1),
-        ptr(out.entropy), ptr(out.entropy_pen), ptr(out.lse), ptr(out.gate),
+        ptr(out.entropy), ptr(out.entropy_f32), ptr(out.entropy_pen), ptr(out.lse), ptr(out.gate),
         ptr(out.topk_ids), ptr(out.topk_lp), ptr(out.sample), stream_handle(dev),
     )
     check(st, "mentat_row_stats")

@@ -136,13 +136,49 @@ def entropy(x: np.ndarray, temperature: float = 1.0) -> float:
     return float(-t.sum())
 
 
+LOG2E_F32 = np.float32(1.4426950408889634)
+
+
+def _softmax_state(y: np.ndarray):
+    """(m, fl(y - m), s, ln s) of a row of dtype values, as torch's device softmax and
+    log_softmax form them: e = exp2(fl(y - m) * fl(log2 e)), s = sum e (here exact in
+    float64, rounded to float once; torch sums in float in its own order)."""
+    m = np.float32(y.max())
+    d = (y - m).astype(np.float32)
+    e = np.exp2(d * LOG2E_F32).astype(np.float32)
+    s = np.float32(e.astype(np.float64).sum())
+    return m, d, e, s, np.float32(np.log(s))
+
+
+def entropy_chain(x: np.ndarray, temperature: float, dtype: str) -> float:
+    """compute_entropy (core/generator_utils.py:196-202) with the rounding torch's
+    device kernels give it in the logits dtype (the reference calls it on bf16
+    logits for a bf16 model, core/generator.py:342, :293):
+      y = rnd(x * fl(1/T))            (a tensor divided by a Python float is
+                                        multiplied by the float reciprocal)
+      p = rnd(e / s), lp = rnd(fl(y - m) - ln s)   (softmax, log_softmax)
+      t = rnd(p * lp), NaN -> 0       (probs * log_probs, nan_to_num)
+      H = -rnd(sum t)                 (the sum exact in float64, rounded once)
+    rnd rounds to `dtype` (identity for f32). Returns H as a Python float."""
+    x = np.asarray(x, dtype=np.float32)
+    inv = np.float32(1.0) / np.float32(temperature)
+    y = round_to(x * inv, dtype)
+    _, d, e, s, logs = _softmax_state(y)
+    with np.errstate(invalid="ignore", divide="ignore"):
+        p = round_to((e / s).astype(np.float32), dtype)
+        lp = round_to((d - logs).astype(np.float32), dtype)
+        t = round_to((p * lp).astype(np.float32), dtype)
+    t = np.where(np.isnan(t), np.float32(0.0), t)
+    S = np.float32(t.astype(np.float64).sum())
+    return float(-round_to(np.array([S], dtype=np.float32), dtype)[0])
+
+
 def log_softmax_keys(xp: np.ndarray, dtype: str) -> np.ndarray:
-    """log_softmax as torch forms it, rounded to the logits dtype (float32 values)."""
+    """log_softmax as torch's device kernel forms it, rounded to the logits dtype
+    (float32 values): rnd(fl(x - m) - ln s), s from _softmax_state."""
     xp = np.asarray(xp, dtype=np.float32)
-    m = np.float32(xp.max())
-    s = np.exp((xp - m).astype(np.float64)).sum()
-    logsum = np.float32(math.log(s))
-    return round_to((xp - m).astype(np.float32) - logsum, dtype)
+    _, d, _, _, logs = _softmax_state(xp)
+    return round_to((d - logs).astype(np.float32), dtype)
 
 
 def topk(keys: np.ndarray, k: int):

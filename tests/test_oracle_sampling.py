@@ -43,6 +43,58 @@ def test_entropy_closed_forms():
     assert abs(S.entropy(np.zeros(5), temperature=0.3) - math.log(5)) < 1e-12
 
 
+def _dtype_ulp(v: float, dtype: str) -> float:
+    """One unit in the last place of the dtype at |v| (normal range)."""
+    bits = {"f32": 23, "bf16": 7, "f16": 10}[dtype]
+    return 2.0 ** (math.floor(math.log2(abs(v))) - bits) if v else 0.0
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16", "f16"])
+def test_entropy_chain_closed_forms(dtype):
+    """The dtype chain of compute_entropy on rows whose terms are known in closed
+    form: a uniform row (every p = rnd(1/V), lp = rnd(-ln V)) gives exactly
+    -rnd(V * rnd(p * lp)); one dominant logit gives 0; a two-value row gives the
+    rounded two-term sum."""
+    V = 32000
+    got = S.entropy_chain(np.zeros(V, dtype=np.float32), 0.7, dtype)
+    p = S.round_to(np.array([1.0 / np.float32(V)], dtype=np.float32), dtype)
+    lp = S.round_to(np.array([-np.log(np.float32(V))], dtype=np.float32), dtype)
+    t = S.round_to(p * lp, dtype)
+    want = -float(S.round_to(np.array([np.float32(V * np.float64(t[0]))]), dtype)[0])
+    assert got == want
+    assert abs(got - math.log(V)) <= 2 * _dtype_ulp(math.log(V), dtype) + 1e-6
+    x = np.zeros(V, dtype=np.float32)
+    x[7] = 1e4
+    assert S.entropy_chain(x, 1.0, dtype) == 0.0
+    # two values: n1 tokens at 1.0, the rest at 0.0 (T = 1)
+    x = np.zeros(1000, dtype=np.float32)
+    x[:10] = 1.0
+    e1, e0 = np.exp2(np.float32(0.0) * S.LOG2E_F32), np.exp2(np.float32(-1.0) * S.LOG2E_F32)
+    s = np.float32(10 * np.float64(e1) + 990 * np.float64(e0))
+    logs = np.log(s)
+    terms = []
+    for e, d, n in ((e1, np.float32(0.0), 10), (e0, np.float32(-1.0), 990)):
+        pr = S.round_to(np.array([e / s], dtype=np.float32), dtype)
+        lq = S.round_to(np.array([d - logs], dtype=np.float32), dtype)
+        terms.append(n * np.float64(S.round_to(pr * lq, dtype)[0]))
+    want = -float(S.round_to(np.array([np.float32(sum(terms))]), dtype)[0])
+    assert S.entropy_chain(x, 1.0, dtype) == want
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16", "f16"])
+def test_entropy_chain_within_a_unit_of_float64(dtype):
+    """Rounding every step to the dtype moves H by at most about one unit of the
+    dtype from the float64 entropy of the same values (random rows, T = 0.7 and 1)."""
+    rng = np.random.default_rng(3)
+    tdt = {"f32": torch.float32, "bf16": torch.bfloat16, "f16": torch.float16}[dtype]
+    for trial in range(6):
+        x = torch.from_numpy(rng.normal(0, 0.5 + trial, 20000).astype(np.float32)).to(tdt).float().numpy()
+        for T in (0.7, 1.0):
+            H64 = S.entropy(S.round_to(x * (np.float32(1.0) / np.float32(T)), dtype), 1.0)
+            Hc = S.entropy_chain(x, T, dtype)
+            assert abs(Hc - H64) <= 2 * _dtype_ulp(H64, dtype) + 1e-5, (dtype, trial, T, Hc, H64)
+
+
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
 def test_entropy_and_keys_against_torch(dtype):
     rng = np.random.default_rng(0)
