@@ -21,11 +21,17 @@
 // lazy: the running max only moves when some column's tile max exceeds it by
 // more than 8 (probabilities stay <= 2^8 otherwise, exact in fp32/16-bit).
 //
-// Work partition (stream-K): all (sequence, kv head, tile) triples are laid
-// out in one flat index space; each of the W persistent wavefronts takes an
-// equal contiguous range. A wavefront whose range covers a whole (sequence,
-// kv head) unit writes the output directly; split units leave (m, l, O)
-// partials in the workspace at slot unit + wave, merged by combine_kernel.
+// Work partition (stream-K): the (sequence, head unit, tile) triples are laid
+// out in one flat index space, split into equal contiguous ranges. With Hkv a
+// multiple of 4 a head unit is a team of 4 kv heads and the ranges go to the W/4
+// persistent workgroups: the 4 waves of a workgroup take the 4 heads of the same
+// tiles, so the workgroup reads each page's K (and V) of those heads as one
+// contiguous 16 KiB piece at a time (the native store holds a page's heads next
+// to each other), which the memory system serves faster than 4 KiB pieces of
+// unrelated pages. Otherwise a head unit is one kv head and each of the W waves
+// takes a range. A range that covers a whole (sequence, kv head) unit writes the
+// output directly; split units leave (m, l, O) partials in the workspace, merged
+// inside the kernel by the last piece to arrive.
 #include "mentat_common.h"
 
 namespace mentat {
@@ -79,6 +85,7 @@ struct NativeParams {
   float* ws_ml;      // [slots][G][2]
   int32_t* ctr;      // [N*Hkv] arrival counters of split units (zero between calls)
   int N, Hq, Hkv, B, W;
+  int TW;            // kv heads per head unit: 4 (a workgroup's waves share tiles) or 1
   float scale_log2;
 };
 
@@ -92,33 +99,21 @@ __device__ __forceinline__ int seq_len_of(const NativeParams& p, int s) {
   return n > 0 ? n : 0;
 }
 
-// Block-wide tile prefix over the N sequences into s_prefix[0..N].
-__device__ void tile_prefix(const NativeParams& p, int32_t* s_prefix, int32_t* s_scan) {
-  const int tid = threadIdx.x;
-  const int per = (p.N + kNativeThreads - 1) / kNativeThreads;
-  const int base = tid * per;
-  int loc = 0;
-  for (int i = 0; i < per; ++i) {
-    const int s = base + i;
-    if (s < p.N) loc += (seq_len_of(p, s) + 15) >> 4;
-  }
-  s_scan[tid] = loc;
-  __syncthreads();
-  for (int off = 1; off < kNativeThreads; off <<= 1) {
-    const int v = tid >= off ? s_scan[tid - off] : 0;
-    __syncthreads();
-    s_scan[tid] += v;
-    __syncthreads();
-  }
-  int run = s_scan[tid] - loc;
-  for (int i = 0; i < per; ++i) {
-    const int s = base + i;
-    if (s < p.N) {
-      s_prefix[s] = run;
-      run += (seq_len_of(p, s) + 15) >> 4;
+// Tile prefix over the N sequences into s_prefix[0..N]: wave 0 scans 64
+// sequences at a time with DPP prefix sums; one barrier publishes it.
+__device__ void tile_prefix(const NativeParams& p, int32_t* s_prefix) {
+  if (threadIdx.x < 64) {
+    const int lane = threadIdx.x;
+    uint32_t carry = 0;
+    for (int b = 0; b < p.N; b += 64) {
+      const int s = b + lane;
+      const uint32_t t = s < p.N ? (uint32_t)((seq_len_of(p, s) + 15) >> 4) : 0u;
+      const uint32_t inc = wave_incl_scan_u32(t) + carry;
+      if (s < p.N) s_prefix[s] = (int32_t)(inc - t);
+      carry = (uint32_t)__builtin_amdgcn_readlane((int)inc, 63);
     }
+    if (lane == 0) s_prefix[p.N] = (int32_t)carry;
   }
-  if (tid == kNativeThreads - 1) s_prefix[p.N] = s_scan[kNativeThreads - 1];
   __syncthreads();
 }
 
@@ -169,13 +164,14 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t partial_rsrc(const NativeParam
   return make_rsrc(p.ws_o, (int)(bytes < 0x7fffffffL ? bytes : 0x7fffffffL));
 }
 
-// Pieces are the partial slots unit + w of waves w0..w1; lane l owns the
-// E = G*D/64 consecutive outputs starting at l*E of the unit's [G][D] block.
+// Pieces are the partial slots (hunit + e) * TW + wsub of the partition
+// entities e = w0..w1 (waves or workgroups) that covered the unit; lane l owns
+// the E = G*D/64 consecutive outputs starting at l*E of the unit's [G][D] block.
 // Pieces are read in batches whose loads are all in flight together, and are
-// combined in wave order, so the result does not depend on arrival order.
+// combined in entity order, so the result does not depend on arrival order.
 template <typename T, int D, int G>
-__device__ __forceinline__ void merge_unit(const NativeParams& p, int seq, int head, long unit, int w0, int w1,
-                                           int lane) {
+__device__ __forceinline__ void merge_unit(const NativeParams& p, int seq, int head, long hunit, int wsub, int w0,
+                                           int w1, int lane) {
   constexpr int E = G * D / 64;
   static_assert(E >= 1, "merge lane split");
   constexpr int KB = E >= 32 ? 1 : (E >= 16 ? 2 : 4);  // pieces per batch
@@ -190,7 +186,7 @@ __device__ __forceinline__ void merge_unit(const NativeParams& p, int seq, int h
     float mk[KB], lk[KB], ok[KB][E];
     // Past-the-end entries of the last batch reload piece n-1 and are dropped.
     static_for<KB>([&](auto i) {
-      const long slot = unit + w0 + min(k0 + (int)i, n - 1);
+      const long slot = (hunit + w0 + min(k0 + (int)i, n - 1)) * p.TW + wsub;
       mk[i] = get_shared(p.ws_ml + (slot * G + g) * 2);
       lk[i] = get_shared(p.ws_ml + (slot * G + g) * 2 + 1);
       if constexpr (E % 4 == 0) {
@@ -239,37 +235,45 @@ __global__ __launch_bounds__(kNativeThreads) void paged_decode_mfma_kernel(Nativ
   using S = typename T::storage;
 
   __shared__ int32_t s_prefix[kNativeMaxN + 1];
-  __shared__ int32_t s_scan[kNativeThreads];
-  tile_prefix(p, s_prefix, s_scan);
+  tile_prefix(p, s_prefix);
 
-  const int T_total = uniform(p.Hkv * s_prefix[p.N]);
-  const int tpw = (T_total + p.W - 1) / p.W;
+  const int TW = p.TW, HU = p.Hkv / TW;              // head units per sequence
+  const int PE = p.W / TW;                           // partition entities (waves or workgroups)
+  const int T_total = uniform(HU * s_prefix[p.N]);
+  // Equal static ranges, one per partition entity. (Claiming a dynamic tail in
+  // chunks did not pay: a chunk's first-tile latency and partial publish cost
+  // 2-3 us, as much as the spread it was meant to absorb.)
+  const int stat = (T_total + PE - 1) / PE;
+  auto range_of = [&](int x) -> int { return x / stat; };
   const int lane = threadIdx.x & 63;
   const int wv = uniform(blockIdx.x * (kNativeThreads / 64) + (threadIdx.x >> 6));
+  const int pe = TW == 1 ? wv : (int)blockIdx.x;
+  const int wsub = TW == 1 ? 0 : uniform(threadIdx.x >> 6);  // this wave's head within the unit
   // Sequences without cached tokens get zeros (no tile covers them).
   for (int s = wv; s < p.N; s += p.W) {
     if (s_prefix[s + 1] == s_prefix[s]) {
       for (int e = lane; e < p.Hq * D; e += 64) Elem<T>::store1(p.out, (long)s * p.Hq * D + e, 0.f);
     }
   }
-  int f = wv * tpw;
-  const int fend = min(T_total, f + tpw);
+  int f = min(T_total, pe * stat);
+  const int fend = min(T_total, (pe + 1) * stat);
   if (f >= fend) return;
 
-  // Unit containing f: last s with Hkv*prefix[s] <= f (upper_bound - 1).
+  // Unit containing f: last s with HU*prefix[s] <= f (upper_bound - 1).
   int seq;
   {
     int lo = 0, hi = p.N;
     while (lo < hi) {
       const int mid = (lo + hi) >> 1;
-      if (p.Hkv * s_prefix[mid] <= f) lo = mid + 1; else hi = mid;
+      if (HU * s_prefix[mid] <= f) lo = mid + 1; else hi = mid;
     }
     seq = uniform(lo - 1);
   }
   int pre = uniform(s_prefix[seq]);
   int nt = uniform(s_prefix[seq + 1]) - pre;
-  int head = (f - p.Hkv * pre) / nt;
-  int tile = (f - p.Hkv * pre) - head * nt;
+  int hu = (f - HU * pre) / nt;
+  int tile = (f - HU * pre) - hu * nt;
+  int head = hu * TW + wsub;
 
   const int lr = lane & 15;  // tile row (K operand) / column (S^T, Q^T, O)
   const int lg = lane >> 4;  // 4-lane-group index
@@ -278,7 +282,7 @@ __global__ __launch_bounds__(kNativeThreads) void paged_decode_mfma_kernel(Nativ
   const int v_lane = lr * B + 4 * lg;      // V [D][B] page-head: dim lr, tokens 4*lg..
 
   while (f < fend) {
-    const int ustart = p.Hkv * pre + head * nt;
+    const int ustart = HU * pre + hu * nt;
     const int uend = ustart + nt;
     const int seg_end = min(fend, uend);
     const int t_first = tile;
@@ -405,7 +409,8 @@ __global__ __launch_bounds__(kNativeThreads) void paged_decode_mfma_kernel(Nativ
         }
       }
     } else {
-      const long slot = unit + wv;
+      const long hunit = (long)seq * HU + hu;
+      const long slot = (hunit + pe) * TW + wsub;
       const __amdgpu_buffer_rsrc_t rw = partial_rsrc(p, G, D);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -426,13 +431,13 @@ __global__ __launch_bounds__(kNativeThreads) void paged_decode_mfma_kernel(Nativ
       }
       // Arrival: the piece's stores complete, then it is counted; the unit's
       // last piece merges them all.
-      const int w0 = ustart / tpw, w1 = (uend - 1) / tpw;
+      const int w0 = range_of(ustart), w1 = range_of(uend - 1);  // the ranges that hold the unit's pieces
       __builtin_amdgcn_s_waitcnt(0);
       int old = 0;
       if (lane == 0) old = __hip_atomic_fetch_add(p.ctr + unit, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       old = __shfl(old, 0);
       if (old == w1 - w0) {
-        merge_unit<T, D, G>(p, seq, head, unit, w0, w1, lane);
+        merge_unit<T, D, G>(p, seq, head, hunit, wsub, w0, w1, lane);
         if (lane == 0) __hip_atomic_store(p.ctr + unit, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
     }
@@ -440,10 +445,10 @@ __global__ __launch_bounds__(kNativeThreads) void paged_decode_mfma_kernel(Nativ
     f = seg_end;
     if (f >= fend) break;
     // Next unit (skip sequences without tokens).
-    ++head;
+    ++hu;
     tile = 0;
-    if (head == p.Hkv) {
-      head = 0;
+    if (hu == HU) {
+      hu = 0;
       ++seq;
       while (seq < p.N && s_prefix[seq + 1] == s_prefix[seq]) ++seq;
       if (seq >= p.N) break;
@@ -451,6 +456,7 @@ __global__ __launch_bounds__(kNativeThreads) void paged_decode_mfma_kernel(Nativ
       pre = uniform(s_prefix[seq]);
       nt = uniform(s_prefix[seq + 1]) - pre;
     }
+    head = hu * TW + wsub;
   }
 }
 
@@ -565,6 +571,7 @@ int native_paged_decode(const void* q, const void* k_cache, const void* v_cache,
   const int G = Hq / Hkv;
   p.N = N; p.Hq = Hq; p.Hkv = Hkv; p.B = block_size; p.W = workspace_waves(D, G);
   if (p.W <= 0) return MENTAT_EUNSUP;
+  p.TW = (Hkv % 4 == 0) ? 4 : 1;
   p.scale_log2 = scale * kLog2e;
   const size_t slots = (size_t)N * Hkv + p.W;
   p.ctr = (int32_t*)workspace;

@@ -180,22 +180,6 @@ struct RowSharedT {
 };
 using RowShared = RowSharedT<kRowWaves>;
 
-// ---- wave-wide sums, minima and prefix sums through DPP (register moves, no LDS round trip) ----
-constexpr int kDppRowShr1 = 0x111, kDppRowShr2 = 0x112, kDppRowShr3 = 0x113, kDppRowShr4 = 0x114,
-              kDppRowShr8 = 0x118, kDppRowBcast15 = 0x142, kDppRowBcast31 = 0x143;
-// Lanes whose row / bank is masked off, or that have no source lane, read 0.
-template <int CTRL, int RM = 0xF, int BM = 0xF>
-__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
-  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, RM, BM, true);
-}
-template <int CTRL, int RM = 0xF, int BM = 0xF>
-__device__ __forceinline__ uint64_t dpp_u64(uint64_t v) {
-  return ((uint64_t)dpp_u32<CTRL, RM, BM>((uint32_t)(v >> 32)) << 32) | dpp_u32<CTRL, RM, BM>((uint32_t)v);
-}
-template <int CTRL>
-__device__ __forceinline__ double dpp_f64(double v) {
-  return __builtin_bit_cast(double, dpp_u64<CTRL>(__builtin_bit_cast(uint64_t, v)));
-}
 // Butterflies within each row of 16 lanes: every lane then holds its row's total.
 template <typename T, class MOVE>
 __device__ __forceinline__ T row_total(T v, MOVE mv) {
@@ -204,10 +188,6 @@ __device__ __forceinline__ T row_total(T v, MOVE mv) {
   v += mv(v, std::integral_constant<int, kDppRowHalfMirror>{});
   v += mv(v, std::integral_constant<int, kDppRowMirror>{});
   return v;
-}
-__device__ __forceinline__ uint32_t rl32(uint32_t v, int l) { return (uint32_t)__builtin_amdgcn_readlane((int)v, l); }
-__device__ __forceinline__ uint64_t rl64(uint64_t v, int l) {
-  return ((uint64_t)rl32((uint32_t)(v >> 32), l) << 32) | rl32((uint32_t)v, l);
 }
 // Wave totals (wave-uniform), the four row totals added in row order.
 __device__ __forceinline__ uint32_t wave_sum_u32(uint32_t v) {
@@ -231,20 +211,6 @@ __device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
   v = min(v, (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, kDppRowMirror, 0xF, 0xF, false));
   return min(min(rl32(v, 0), rl32(v, 16)), min(rl32(v, 32), rl32(v, 48)));
 }
-// Inclusive prefix sum over the wave's lanes (lane order): window sums within rows, then the
-// row totals carried across rows by row broadcasts.
-__device__ __forceinline__ uint64_t wave_incl_scan_u64(uint64_t v) {
-  const uint64_t v0 = v;
-  v += dpp_u64<kDppRowShr1>(v0);
-  v += dpp_u64<kDppRowShr2>(v0);
-  v += dpp_u64<kDppRowShr3>(v0);
-  v += dpp_u64<kDppRowShr4, 0xF, 0xE>(v);
-  v += dpp_u64<kDppRowShr8, 0xF, 0xC>(v);
-  v += dpp_u64<kDppRowBcast15, 0xA, 0xF>(v);
-  v += dpp_u64<kDppRowBcast31, 0xC, 0xF>(v);
-  return v;
-}
-
 __device__ __forceinline__ float wave_max(float v) {
 _Pragma("clang loop unroll(full)")
   for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
