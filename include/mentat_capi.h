@@ -74,6 +74,12 @@ int mentat_device_count(void);
  * Semantics: for sequence i, query head h attends to ALL of its cached
  * tokens (the token appended this step included) with kv head
  * h / (Hq/Hkv) and softmax scale `scale`:  out[i,h] = softmax(q·Kᵀ·scale)·V.
+ * window_size > 0 restricts sequence i of length len to its last window_size
+ * tokens, [max(0, len - window_size), len): the reference's window argument
+ * (attention_backend.py:192-229), which flash_attn_varlen_func applies as
+ * window_size=(window_size - 1, 0) with the query aligned to the end of its
+ * keys. 0 attends to all tokens (the reference's window_size=None); negative
+ * values return MENTAT_EINVAL.
  *
  * `layout` selects the pool layout (MENTAT_LAYOUT_*). The native layout runs
  * on the MFMA kernel with a persistent, equal-work (stream-K) partition of all
@@ -95,14 +101,14 @@ int mentat_device_count(void);
  * than read.
  * ---------------------------------------------------------------------- */
 size_t mentat_paged_decode_workspace_bytes(int layout, int N, int Hq, int Hkv, int D, int block_size,
-                                           int max_seqlen, int chunk_tokens);
+                                           int max_seqlen, int window_size, int chunk_tokens);
 
 int mentat_paged_decode(int layout, const void* q, const void* k_cache, const void* v_cache,
                         const int32_t* block_tables, int64_t table_stride,
                         const int32_t* seq_rows, const int32_t* seq_lens,
                         const int32_t* cu_seqlens_k, int64_t num_blocks,
                         void* out, int N, int Hq, int Hkv, int D, int block_size,
-                        int max_seqlen, float scale, int dtype, int chunk_tokens,
+                        int max_seqlen, int window_size, float scale, int dtype, int chunk_tokens,
                         void* workspace, size_t workspace_bytes, void* stream);
 
 /* The chunk length (tokens) the reference-layout path uses when chunk_tokens == 0. */
@@ -125,7 +131,8 @@ int mentat_paged_decode_noalloc(int layout, const void* q, const void* k_cache, 
                                 const int32_t* seq_rows, const int32_t* seq_lens,
                                 const int32_t* cu_seqlens_k, int64_t num_blocks,
                                 void* out, int N, int Hq, int Hkv, int D, int block_size,
-                                int max_seqlen, float scale, int dtype, int chunk_tokens, void* stream);
+                                int max_seqlen, int window_size, float scale, int dtype, int chunk_tokens,
+                                void* stream);
 
 /* ------------------------------------------------------------------------
  * Prefix-tree decode attention: the same result as mentat_paged_decode for

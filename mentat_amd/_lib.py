@@ -37,7 +37,7 @@ _c_u32 = ctypes.c_uint32
 SIGNATURES: dict[str, tuple] = {
     "mentat_abi_version": (_c_int, []),
     "mentat_device_count": (_c_int, []),
-    "mentat_paged_decode_workspace_bytes": (_c_size, [_c_int] * 8),
+    "mentat_paged_decode_workspace_bytes": (_c_size, [_c_int] * 9),
     "mentat_paged_decode_auto_chunk": (_c_int, [_c_int] * 4),
     "mentat_paged_decode": (
         _c_int,
@@ -48,7 +48,7 @@ SIGNATURES: dict[str, tuple] = {
             _c_void_p, _c_void_p,  # seq_rows, seq_lens
             _c_void_p, _c_i64,  # cu_seqlens_k, num_blocks
             _c_void_p, _c_int, _c_int, _c_int, _c_int, _c_int,  # out, N, Hq, Hkv, D, block_size
-            _c_int, _c_float, _c_int, _c_int,  # max_seqlen, scale, dtype, chunk_tokens
+            _c_int, _c_int, _c_float, _c_int, _c_int,  # max_seqlen, window_size, scale, dtype, chunk_tokens
             _c_void_p, _c_size, _c_void_p,  # workspace, workspace_bytes, stream
         ],
     ),
@@ -61,7 +61,7 @@ SIGNATURES: dict[str, tuple] = {
             _c_void_p, _c_void_p,  # seq_rows, seq_lens
             _c_void_p, _c_i64,  # cu_seqlens_k, num_blocks
             _c_void_p, _c_int, _c_int, _c_int, _c_int, _c_int,  # out, N, Hq, Hkv, D, block_size
-            _c_int, _c_float, _c_int, _c_int,  # max_seqlen, scale, dtype, chunk_tokens
+            _c_int, _c_int, _c_float, _c_int, _c_int,  # max_seqlen, window_size, scale, dtype, chunk_tokens
             _c_void_p,  # stream
         ],
     ),

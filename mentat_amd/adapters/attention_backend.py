@@ -80,18 +80,22 @@ def attn_decode(
     N: int,
     window_size: Optional[int] = None,
 ) -> torch.Tensor:
-    """One query per sequence over its whole cached context (reference semantics:
-    the token appended this step included, default scale head_dim**-0.5)."""
-    if window_size is not None:
-        raise NotImplementedError("attn_decode: sliding-window decode is not supported")
+    """One query per sequence over its cached context (reference semantics: the
+    token appended this step included, default scale head_dim**-0.5). With
+    window_size w, sequence i of length len attends to its last w tokens,
+    [max(0, len - w), len): the reference's flash path
+    (adapters/attention_backend.py:219-228, window_size=(w - 1, 0) with the
+    query aligned to the end of the keys). The reference's SDPA fallback
+    (:99-168) ignores the window; the two agree whenever len <= w, which
+    trim_to_window keeps true."""
     q = q.contiguous()
     if isinstance(k, PagedKVView):
         if not isinstance(v, PagedKVView):
             raise TypeError("attn_decode: k and v must both be PagedKVView or both tensors")
         return ops.paged_decode(
             q, k.store, v.store, layout=k.layout, block_tables=k.tables, seq_lens=k.lens, seq_rows=k.rows,
-            max_seqlen=max(int(max_seqlen_k), 1),
+            max_seqlen=max(int(max_seqlen_k), 1), window_size=window_size,
         )
     cu = cu_seqlens_k.to(device=q.device, dtype=torch.int32)
     return ops.paged_decode(q, k.contiguous(), v.contiguous(), cu_seqlens_k=cu,
-                            max_seqlen=max(int(max_seqlen_k), 1))
+                            max_seqlen=max(int(max_seqlen_k), 1), window_size=window_size)

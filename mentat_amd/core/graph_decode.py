@@ -315,7 +315,7 @@ class DecodeGraphs:
         a, m = self.a, self.m
         nbytes = get_lib().mentat_paged_decode_workspace_bytes(
             m.layout, self.max_batch, a.num_attention_heads, a.num_key_value_heads, a.head_dim, m.block_size,
-            m._pages_cap * m.block_size, 0)
+            m._pages_cap * m.block_size, 0, 0)
         with torch.cuda.stream(self._stream):
             self._ws = ops.workspace(self.dev, nbytes)
 

@@ -258,7 +258,12 @@ class PagedKVCacheManager:
     def allocate_sequence(self) -> int:
         seq_id = self._next_seq_id
         self._next_seq_id += 1
-        self._sequences[seq_id] = SequenceState(seq_id=seq_id, num_layers=self.num_layers, row=self._take_row())
+        row = self._take_row()
+        self._sequences[seq_id] = SequenceState(seq_id=seq_id, num_layers=self.num_layers, row=row)
+        if self.device.type == "cuda":
+            # a reused row still holds its previous sequence's lengths: the new
+            # sequence has no tokens until its first append
+            self._lens[:, row] = 0
         return seq_id
 
     def fork_sequence(self, parent_id: int) -> int:

@@ -22,6 +22,12 @@
 // Split-K: when a launch has more than one chunk per sequence, each unit writes
 // its (m, l, acc) to the workspace and combine_kernel merges them with the usual
 // log-sum-exp rescaling.
+//
+// Sliding window (window > 0): a sequence of length len attends to its tokens
+// [max(0, len - window), len), the last `window` of them, as
+// flash_attn_varlen_func(causal=True, window_size=(window - 1, 0)) does for one
+// query aligned to the end of its keys (adapters/attention_backend.py:219-228).
+// The chunks start at the window's first token.
 #include <mutex>
 
 #include "mentat_common.h"
@@ -42,8 +48,14 @@ struct DecodeParams {
   float* ws_acc;  // [N, Hq, max_chunks, D]
   float* ws_ml;   // [N, Hq, max_chunks, 2]
   int N, Hq, Hkv, block_size, chunk_tokens, max_chunks;
+  int window;        // attend to the last `window` tokens; 0 = all of them
   float scale_log2;  // softmax scale * log2(e)
 };
+
+// First token a sequence of length len attends to.
+__device__ __forceinline__ int window_start(int len, int window) {
+  return window > 0 && len > window ? len - window : 0;
+}
 
 constexpr int kWavesPerBlock = 4;
 
@@ -74,7 +86,7 @@ __global__ __launch_bounds__(kWavesPerBlock * 64) void paged_decode_kernel(Decod
     base_tok = p.cu[seq];
     len = p.cu[seq + 1] - base_tok;
   }
-  const int t0 = chunk * p.chunk_tokens;
+  const int t0 = window_start(len, p.window) + chunk * p.chunk_tokens;
   if (t0 >= len && chunk > 0) return;  // empty chunk (chunk 0 always writes a state)
   const int t1 = min(len, t0 + p.chunk_tokens);
 
@@ -203,7 +215,8 @@ __global__ __launch_bounds__(64) void decode_combine_kernel(DecodeParams p) {
   } else {
     len = p.cu[seq + 1] - p.cu[seq];
   }
-  const int nch = max(1, min(p.max_chunks, (len + p.chunk_tokens - 1) / p.chunk_tokens));
+  const int span = len - window_start(len, p.window);
+  const int nch = max(1, min(p.max_chunks, (span + p.chunk_tokens - 1) / p.chunk_tokens));
   const long slot0 = ((long)seq * p.Hq + qh) * p.max_chunks;
   float mx = kNegInf;
   for (int c = 0; c < nch; ++c) mx = fmaxf(mx, p.ws_ml[(slot0 + c) * 2]);
@@ -293,14 +306,22 @@ size_t native_workspace_bytes(int N, int Hq, int Hkv, int D);
 int native_paged_decode(const void* q, const void* k_cache, const void* v_cache, const int32_t* block_tables,
                         int64_t table_stride, const int32_t* seq_rows, const int32_t* seq_lens,
                         int64_t num_blocks, void* out, int N, int Hq, int Hkv, int D, int block_size,
-                        float scale, int dtype, void* workspace, size_t workspace_bytes, hipStream_t stream);
+                        int window_size, float scale, int dtype, void* workspace, size_t workspace_bytes,
+                        hipStream_t stream);
+
+// Longest attended span: the window caps it.
+static int attended_span(int max_seqlen, int window) {
+  return window > 0 && window < max_seqlen ? window : max_seqlen;
+}
 
 extern "C" size_t mentat_paged_decode_workspace_bytes(int layout, int N, int Hq, int Hkv, int D,
-                                                      int block_size, int max_seqlen, int chunk_tokens) {
-  if (N <= 0 || Hq <= 0 || Hkv <= 0 || D <= 0 || max_seqlen <= 0) return 0;
+                                                      int block_size, int max_seqlen, int window_size,
+                                                      int chunk_tokens) {
+  if (N <= 0 || Hq <= 0 || Hkv <= 0 || D <= 0 || max_seqlen <= 0 || window_size < 0) return 0;
   if (layout == MENTAT_LAYOUT_NATIVE) return native_workspace_bytes(N, Hq, Hkv, D);
-  const int chunk = chunk_tokens > 0 ? chunk_tokens : auto_chunk(N, Hkv, block_size, max_seqlen);
-  const int mc = ceil_div(max_seqlen, chunk);
+  const int span = attended_span(max_seqlen, window_size);
+  const int chunk = chunk_tokens > 0 ? chunk_tokens : auto_chunk(N, Hkv, block_size, span);
+  const int mc = ceil_div(span, chunk);
   if (mc <= 1) return 0;
   return kWsReserved + (size_t)N * Hq * mc * (D + 2) * sizeof(float);
 }
@@ -310,28 +331,28 @@ extern "C" int mentat_paged_decode(int layout, const void* q, const void* k_cach
                                    const int32_t* seq_rows, const int32_t* seq_lens,
                                    const int32_t* cu_seqlens_k, int64_t num_blocks, void* out, int N,
                                    int Hq, int Hkv, int D, int block_size, int max_seqlen,
-                                   float scale, int dtype, int chunk_tokens, void* workspace,
-                                   size_t workspace_bytes, void* stream) {
+                                   int window_size, float scale, int dtype, int chunk_tokens,
+                                   void* workspace, size_t workspace_bytes, void* stream) {
   if (N == 0) return MENTAT_OK;
   if (!q || !k_cache || !v_cache || !out || N < 0 || Hq <= 0 || Hkv <= 0 || D <= 0) return MENTAT_EINVAL;
   if (Hq % Hkv != 0) return MENTAT_EINVAL;
   const bool paged = block_tables != nullptr;
   if (paged && (!seq_lens || block_size <= 0 || table_stride <= 0 || num_blocks <= 0)) return MENTAT_EINVAL;
   if (!paged && !cu_seqlens_k) return MENTAT_EINVAL;
-  if (max_seqlen < 0) return MENTAT_EINVAL;
+  if (max_seqlen < 0 || window_size < 0) return MENTAT_EINVAL;
   if (layout == MENTAT_LAYOUT_NATIVE) {
     if (!paged) return MENTAT_EINVAL;
     return native_paged_decode(q, k_cache, v_cache, block_tables, table_stride, seq_rows, seq_lens, num_blocks,
-                               out, N, Hq, Hkv, D, block_size, scale, dtype, workspace, workspace_bytes,
-                               (hipStream_t)stream);
+                               out, N, Hq, Hkv, D, block_size, window_size, scale, dtype, workspace,
+                               workspace_bytes, (hipStream_t)stream);
   }
   if (layout != MENTAT_LAYOUT_REFERENCE) return MENTAT_EINVAL;
-  const int ms = max_seqlen > 0 ? max_seqlen : 1;
+  const int ms = attended_span(max_seqlen > 0 ? max_seqlen : 1, window_size);
   DecodeParams p;
   p.q = q; p.k = k_cache; p.v = v_cache;
   p.tables = block_tables; p.table_stride = table_stride; p.rows = seq_rows; p.lens = seq_lens;
   p.cu = cu_seqlens_k; p.num_blocks = num_blocks; p.out = out;
-  p.N = N; p.Hq = Hq; p.Hkv = Hkv; p.block_size = block_size;
+  p.N = N; p.Hq = Hq; p.Hkv = Hkv; p.block_size = block_size; p.window = window_size;
   p.chunk_tokens = chunk_tokens > 0 ? chunk_tokens : auto_chunk(N, Hkv, block_size, ms);
   p.max_chunks = ceil_div(ms, p.chunk_tokens);
   p.scale_log2 = scale * kLog2e;
@@ -404,17 +425,19 @@ extern "C" int mentat_paged_decode_noalloc(int layout, const void* q, const void
                                            const int32_t* block_tables, int64_t table_stride,
                                            const int32_t* seq_rows, const int32_t* seq_lens,
                                            const int32_t* cu_seqlens_k, int64_t num_blocks, void* out, int N,
-                                           int Hq, int Hkv, int D, int block_size, int max_seqlen, float scale,
-                                           int dtype, int chunk_tokens, void* stream) {
+                                           int Hq, int Hkv, int D, int block_size, int max_seqlen,
+                                           int window_size, float scale, int dtype, int chunk_tokens,
+                                           void* stream) {
   if (N == 0) return MENTAT_OK;
-  if (N < 0 || Hq <= 0 || Hkv <= 0 || D <= 0 || max_seqlen < 0) return MENTAT_EINVAL;
+  if (N < 0 || Hq <= 0 || Hkv <= 0 || D <= 0 || max_seqlen < 0 || window_size < 0) return MENTAT_EINVAL;
   const size_t need = mentat_paged_decode_workspace_bytes(layout, N, Hq, Hkv, D, block_size,
-                                                          max_seqlen > 0 ? max_seqlen : 1, chunk_tokens);
+                                                          max_seqlen > 0 ? max_seqlen : 1, window_size,
+                                                          chunk_tokens);
   if (need > (size_t)MENTAT_NOALLOC_SCRATCH_BYTES) return MENTAT_ESPACE;
   void* ws = nullptr;
   const int st = scratch_address(&ws, (hipStream_t)stream);
   if (st != MENTAT_OK) return st;
   return mentat_paged_decode(layout, q, k_cache, v_cache, block_tables, table_stride, seq_rows, seq_lens,
-                             cu_seqlens_k, num_blocks, out, N, Hq, Hkv, D, block_size, max_seqlen, scale, dtype,
-                             chunk_tokens, ws, (size_t)MENTAT_NOALLOC_SCRATCH_BYTES, stream);
+                             cu_seqlens_k, num_blocks, out, N, Hq, Hkv, D, block_size, max_seqlen, window_size,
+                             scale, dtype, chunk_tokens, ws, (size_t)MENTAT_NOALLOC_SCRATCH_BYTES, stream);
 }

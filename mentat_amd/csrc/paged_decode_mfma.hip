@@ -32,6 +32,12 @@
 // takes a range. A range that covers a whole (sequence, kv head) unit writes the
 // output directly; split units leave (m, l, O) partials in the workspace, merged
 // inside the kernel by the last piece to arrive.
+//
+// Sliding window (window > 0): a sequence of length len attends to its last
+// `window` tokens, [max(0, len - window), len), as flash_attn_varlen_func with
+// causal=True, window_size=(window - 1, 0) does for one query aligned to the end
+// of its keys (adapters/attention_backend.py:219-228). Its tiles run from the
+// one holding the window's first token; earlier tokens of that tile are masked.
 #include "mentat_common.h"
 
 namespace mentat {
@@ -86,6 +92,7 @@ struct NativeParams {
   int32_t* ctr;      // [N*Hkv] arrival counters of split units (zero between calls)
   int N, Hq, Hkv, B, W;
   int TW;            // kv heads per head unit: 4 (a workgroup's waves share tiles) or 1
+  int window;        // attend to the last `window` tokens; 0 = all of them
   float scale_log2;
 };
 
@@ -99,6 +106,13 @@ __device__ __forceinline__ int seq_len_of(const NativeParams& p, int s) {
   return n > 0 ? n : 0;
 }
 
+// First token a sequence of length n attends to.
+__device__ __forceinline__ int window_lo(int n, int window) { return window > 0 && n > window ? n - window : 0; }
+
+// 16-token tiles a sequence of length n covers: from the tile of its first
+// attended token to the tile of its last.
+__device__ __forceinline__ int tiles_of(int n, int window) { return ((n + 15) >> 4) - (window_lo(n, window) >> 4); }
+
 // Tile prefix over the N sequences into s_prefix[0..N]: wave 0 scans 64
 // sequences at a time with DPP prefix sums; one barrier publishes it.
 __device__ void tile_prefix(const NativeParams& p, int32_t* s_prefix) {
@@ -107,7 +121,7 @@ __device__ void tile_prefix(const NativeParams& p, int32_t* s_prefix) {
     uint32_t carry = 0;
     for (int b = 0; b < p.N; b += 64) {
       const int s = b + lane;
-      const uint32_t t = s < p.N ? (uint32_t)((seq_len_of(p, s) + 15) >> 4) : 0u;
+      const uint32_t t = s < p.N ? (uint32_t)tiles_of(seq_len_of(p, s), p.window) : 0u;
       const uint32_t inc = wave_incl_scan_u32(t) + carry;
       if (s < p.N) s_prefix[s] = (int32_t)(inc - t);
       carry = (uint32_t)__builtin_amdgcn_readlane((int)inc, 63);
@@ -285,10 +299,11 @@ __global__ __launch_bounds__(kNativeThreads) void paged_decode_mfma_kernel(Nativ
     const int ustart = HU * pre + hu * nt;
     const int uend = ustart + nt;
     const int seg_end = min(fend, uend);
-    const int t_first = tile;
-    const int t_last = tile + (seg_end - f);
     const int row = p.rows ? scalar_load(p.rows, seq) : seq;
     const int len = max(scalar_load(p.lens, row), 0);
+    const int lo = window_lo(len, p.window);
+    const int t_first = tile + (lo >> 4);  // absolute tile ids within the sequence
+    const int t_last = t_first + (seg_end - f);
     const int32_t* trow = p.tables + (long)row * p.table_stride;
 
     // Q^T operand: column q = lr holds Q[seq, head*G + q, 32s + 8*lg .. +8].
@@ -339,7 +354,7 @@ __global__ __launch_bounds__(kNativeThreads) void paged_decode_mfma_kernel(Nativ
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         sc[i] = st[i] * p.scale_log2;
-        if (!okb || tok0 + i >= len) sc[i] = kNegInf;
+        if (!okb || (unsigned)(tok0 + i - lo) >= (unsigned)(len - lo)) sc[i] = kNegInf;  // outside [lo, len)
       }
       // m is uniform over the four lanes of a column; a lane compares its own
       // four scores against it, and only when some lane has outgrown it by the
@@ -558,7 +573,8 @@ size_t native_workspace_bytes(int N, int Hq, int Hkv, int D) {
 int native_paged_decode(const void* q, const void* k_cache, const void* v_cache, const int32_t* block_tables,
                         int64_t table_stride, const int32_t* seq_rows, const int32_t* seq_lens,
                         int64_t num_blocks, void* out, int N, int Hq, int Hkv, int D, int block_size,
-                        float scale, int dtype, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+                        int window_size, float scale, int dtype, void* workspace, size_t workspace_bytes,
+                        hipStream_t stream) {
   if (N > kNativeMaxN || (long)N * Hkv > kMaxNativeUnits) return MENTAT_EUNSUP;
   if (block_size != 16 && block_size != 32 && block_size != 64) return MENTAT_EUNSUP;
   if (!block_tables || !seq_lens || table_stride <= 0 || num_blocks <= 0) return MENTAT_EINVAL;
@@ -572,6 +588,7 @@ int native_paged_decode(const void* q, const void* k_cache, const void* v_cache,
   p.N = N; p.Hq = Hq; p.Hkv = Hkv; p.B = block_size; p.W = workspace_waves(D, G);
   if (p.W <= 0) return MENTAT_EUNSUP;
   p.TW = (Hkv % 4 == 0) ? 4 : 1;
+  p.window = window_size;
   p.scale_log2 = scale * kLog2e;
   const size_t slots = (size_t)N * Hkv + p.W;
   p.ctr = (int32_t*)workspace;

@@ -91,6 +91,7 @@ def paged_decode(
     chunk_tokens: int = 0,
     out: Optional[torch.Tensor] = None,
     layout: int = LAYOUT_REFERENCE,
+    window_size: Optional[int] = None,
 ) -> torch.Tensor:
     """One-query-per-sequence attention over a paged (or packed varlen) KV cache.
 
@@ -105,6 +106,10 @@ def paged_decode(
     ``build_packed_kv`` output (core/paged_kv_cache.py:289-368).
 
     ``max_seqlen`` must be >= every sequence length (it sizes the split-K grid).
+    ``window_size`` (positive, or None for the whole context): sequence i of
+    length len attends to its last window_size tokens, [max(0, len - w), len),
+    as flash_attn_varlen_func(causal=True, window_size=(w - 1, 0)) does in the
+    reference's decode (adapters/attention_backend.py:219-228).
     Returns ``out`` [N, Hq, D] in q's dtype.
     """
     _require(q.dim() == 3, f"q must be [N, Hq, D], got {tuple(q.shape)}")
@@ -118,6 +123,8 @@ def paged_decode(
              "q, k_cache and v_cache must be contiguous")
     if scale is None:
         scale = 1.0 / math.sqrt(D)
+    window = 0 if window_size is None else int(window_size)
+    _require(window_size is None or window > 0, "window_size must be positive")
     if layout == LAYOUT_NATIVE:
         _require(block_tables is not None, "the native layout needs block_tables")
         _require(q.dtype in (torch.bfloat16, torch.float16), "the native layout needs a 16-bit dtype")
@@ -164,7 +171,7 @@ def paged_decode(
         return out
     lib = get_lib()
     max_seqlen = max(int(max_seqlen), 1)
-    nbytes = lib.mentat_paged_decode_workspace_bytes(layout, N, Hq, Hkv, D, block_size, max_seqlen,
+    nbytes = lib.mentat_paged_decode_workspace_bytes(layout, N, Hq, Hkv, D, block_size, max_seqlen, window,
                                                      chunk_tokens)
     ws = workspace(dev, nbytes) if nbytes else None
     st = lib.mentat_paged_decode(
@@ -173,7 +180,7 @@ def paged_decode(
         ptr(seq_rows), ptr(seq_lens),
         ptr(cu_seqlens_k), num_blocks,
         ptr(out), N, Hq, Hkv, D, block_size,
-        max_seqlen, float(scale), DTYPE_CODES[q.dtype], int(chunk_tokens),
+        max_seqlen, window, float(scale), DTYPE_CODES[q.dtype], int(chunk_tokens),
         ptr(ws), nbytes, stream_handle(dev),
     )
     check(st, "mentat_paged_decode")

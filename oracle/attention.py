@@ -11,11 +11,16 @@ Restates
     sequence attends to every packed token of that sequence with
     ``is_causal=False`` and the default scale ``D**-0.5``; GQA query head h
     reads kv head ``h // (Hq // Hkv)`` (the expand/reshape at :152-155).
+  * the decode window of the flash path (adapters/attention_backend.py:219-228):
+    ``window_size=(w - 1, 0)`` with ``causal=True`` and one query aligned to the
+    end of its keys keeps a sequence's last ``w`` tokens.
 
 Pinned by (tests/test_oracle_attention.py): one cached token gives o = v;
 identical keys give o = mean(V); a GQA head-mapping probe; agreement with
 torch's own scaled_dot_product_attention in float64 (an independent library
-routine) on random ragged batches.
+routine) on random ragged batches. The window: the last row of the
+reference's sliding-window prefill mask (adapters/attention_backend.py:81-86)
+through torch's SDPA in float64, and w >= len reduces to no window.
 """
 from __future__ import annotations
 
@@ -49,11 +54,12 @@ def gather_packed_kv(k_pool, v_pool, page_tables, num_tokens, block_size):
     return k_pool[b, s], v_pool[b, s], cu, max_len
 
 
-def sdpa_decode_f64(q, packed_k, packed_v, cu_seqlens_k, scale=None):
+def sdpa_decode_f64(q, packed_k, packed_v, cu_seqlens_k, scale=None, window_size=None):
     """Restates adapters/attention_backend.py:99-168 in float64.
 
     q: [N, Hq, D]; packed_k/v: [total, Hkv, D]. Returns [N, Hq, D] float64.
-    A sequence with no cached tokens yields zeros.
+    A sequence with no cached tokens yields zeros. window_size w keeps each
+    sequence's last w tokens (the flash path, :219-228).
     """
     q = np.asarray(q, dtype=np.float64)
     N, Hq, D = q.shape
@@ -64,8 +70,11 @@ def sdpa_decode_f64(q, packed_k, packed_v, cu_seqlens_k, scale=None):
     out = np.zeros((N, Hq, D), dtype=np.float64)
     cu = np.asarray(cu_seqlens_k, dtype=np.int64)
     for i in range(N):
-        k = np.asarray(packed_k[cu[i]:cu[i + 1]], dtype=np.float64)  # [L, Hkv, D]
-        v = np.asarray(packed_v[cu[i]:cu[i + 1]], dtype=np.float64)
+        lo = cu[i]
+        if window_size is not None and cu[i + 1] - cu[i] > window_size:
+            lo = cu[i + 1] - window_size
+        k = np.asarray(packed_k[lo:cu[i + 1]], dtype=np.float64)  # [L, Hkv, D]
+        v = np.asarray(packed_v[lo:cu[i + 1]], dtype=np.float64)
         if k.shape[0] == 0:
             continue
         kh = np.repeat(k, G, axis=1)  # GQA expand: q head h -> kv head h // G
@@ -78,10 +87,10 @@ def sdpa_decode_f64(q, packed_k, packed_v, cu_seqlens_k, scale=None):
     return out
 
 
-def paged_decode_f64(q, k_pool, v_pool, page_tables, num_tokens, block_size, scale=None):
+def paged_decode_f64(q, k_pool, v_pool, page_tables, num_tokens, block_size, scale=None, window_size=None):
     """build_packed_kv followed by the SDPA decode, in float64."""
     pk, pv, cu, _ = gather_packed_kv(k_pool, v_pool, page_tables, num_tokens, block_size)
-    return sdpa_decode_f64(q, pk, pv, cu, scale)
+    return sdpa_decode_f64(q, pk, pv, cu, scale, window_size)
 
 
 def reference_cpu_decode(q, k_pool, v_pool, page_tables, num_tokens, block_size):

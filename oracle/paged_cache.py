@@ -9,6 +9,7 @@ Restates core/paged_kv_cache.py of the reference on plain Python/numpy:
   * ``OracleCache.append``      append_tokens, prefill (:178-225)
   * ``OracleCache.append_batched``  append_tokens_batched, decode (:227-284)
   * ``OracleCache.gather``      build_packed_kv's gather order (:289-368)
+  * ``OracleCache.trim_to_window``  sliding-window eviction (:370-417)
   * ``peak_kv_cache_bytes``     get_stats' formula (:419-439)
 
 Instead of K/V tensors the pools hold integer *tags* (one per written token,
@@ -23,6 +24,10 @@ tags equal its own token history (a fork inherits the history at fork time);
 the K-way branch consequence (first K-1 children in batch order copy, the
 last writes in place); the peak_kv_cache_bytes figure of the reference's
 published run (1316 blocks -> 2,414,870,528 bytes for Qwen3-1.7B).
+trim_to_window (tests/test_trim_to_window.py): the states and tags the
+reference's own manager recorded on scripted scenarios
+(tests/golden/trim_to_window.json), and, where eviction is page-aligned, the
+closed form gather == the last `window` tokens of the history.
 """
 from __future__ import annotations
 
@@ -158,6 +163,38 @@ class OracleCache:
             out.extend(self.pool[layer, b, :k].tolist())
             rem -= k
         return out
+
+    # :370-417
+    def trim_to_window(self, sid: int, window: int) -> None:
+        """Evict all but the last `window` tokens. Whole pages at the front are
+        released; a partially evicted front page has its kept slots moved to
+        the front (in place when private, into a newly allocated page when
+        shared), and later pages are left where they are, exactly as the
+        reference does. The counters become `window`."""
+        if self.ntok[sid][0] <= window:  # :373-374 (layer 0 decides)
+            return
+        for layer in range(self.L):
+            remaining = self.ntok[sid][layer] - window
+            table = self.tables[sid][layer]
+            while remaining > 0 and table:
+                blk = table[0]
+                n_in = min(self.B, remaining)
+                if n_in >= self.B:
+                    table.pop(0)
+                    self.alloc.release(blk)
+                    remaining -= self.B
+                    continue
+                keep = self.B - n_in
+                if self.alloc.is_shared(blk):
+                    new = self.alloc.alloc()
+                    self.pool[layer, new, :keep] = self.pool[layer, blk, n_in:n_in + keep]
+                    self.alloc.release(blk)
+                    table[0] = new
+                else:
+                    self.pool[layer, blk, :keep] = self.pool[layer, blk, n_in:n_in + keep].copy()
+                remaining = 0
+            self.ntok[sid][layer] = window
+            self.tilb[sid][layer] = 0 if window == 0 else (window % self.B or self.B)
 
     def table_entries(self) -> int:
         return sum(len(t) for tables in self.tables.values() for t in tables)

@@ -29,9 +29,14 @@ def test_abi_version_and_pure_host_queries():
     lib = _lib.get_lib()
     assert lib.mentat_abi_version() >= 1
     # Pure host arithmetic: no device needed.
-    assert lib.mentat_paged_decode_workspace_bytes(0, 0, 32, 8, 128, 16, 4096, 0) == 0
-    nb = lib.mentat_paged_decode_workspace_bytes(0, 64, 32, 8, 128, 16, 4096, 256)
+    assert lib.mentat_paged_decode_workspace_bytes(0, 0, 32, 8, 128, 16, 4096, 0, 0) == 0
+    nb = lib.mentat_paged_decode_workspace_bytes(0, 64, 32, 8, 128, 16, 4096, 0, 256)
     assert nb == 262144 + 64 * 32 * 16 * (128 + 2) * 4  # reserved counters + partials
+    # a window caps the attended span: 1024 tokens in chunks of 256 -> 4 chunks per sequence
+    nw = lib.mentat_paged_decode_workspace_bytes(0, 64, 32, 8, 128, 16, 4096, 1024, 256)
+    assert nw == 262144 + 64 * 32 * 4 * (128 + 2) * 4
+    assert lib.mentat_paged_decode_workspace_bytes(0, 64, 32, 8, 128, 16, 4096, 8192, 256) == nb
+    assert lib.mentat_paged_decode_workspace_bytes(0, 64, 32, 8, 128, 16, 4096, -1, 256) == 0
     assert lib.mentat_tree_decode_workspace_bytes(0, 32, 8, 128) == 0
     assert lib.mentat_tree_decode_workspace_bytes(10, 32, 8, 128) == 262144 + 10 * 4 * 130 * 4
     c = lib.mentat_paged_decode_auto_chunk(64, 8, 16, 4096)
@@ -44,10 +49,12 @@ def test_noalloc_entry_refuses_sizes_past_its_scratch():
     scratch before touching the device (pure host arithmetic on the reference
     layout: 64 x 32 heads x 4096 chunks of partials are far past 8 MiB)."""
     lib = _lib.get_lib()
-    need = lib.mentat_paged_decode_workspace_bytes(0, 64, 32, 8, 128, 16, 65536, 16)
+    need = lib.mentat_paged_decode_workspace_bytes(0, 64, 32, 8, 128, 16, 65536, 0, 16)
     assert need > 8388608
     st = lib.mentat_paged_decode_noalloc(0, None, None, None, None, 4096, None, None, None, 65536, None,
-                                         64, 32, 8, 128, 16, 65536, 0.088, 2, 16, None)
+                                         64, 32, 8, 128, 16, 65536, 0, 0.088, 2, 16, None)
     assert st == _lib.MENTAT_ESPACE
     assert lib.mentat_paged_decode_noalloc(0, None, None, None, None, 1, None, None, None, 1, None,
-                                           -1, 32, 8, 128, 16, 16, 0.088, 2, 0, None) == _lib.MENTAT_EINVAL
+                                           -1, 32, 8, 128, 16, 16, 0, 0.088, 2, 0, None) == _lib.MENTAT_EINVAL
+    assert lib.mentat_paged_decode_noalloc(0, None, None, None, None, 1, None, None, None, 1, None,
+                                           4, 32, 8, 128, 16, 16, -2, 0.088, 2, 0, None) == _lib.MENTAT_EINVAL

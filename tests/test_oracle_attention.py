@@ -91,6 +91,43 @@ def test_against_torch_sdpa_float64(Hq, Hkv, D):
         np.testing.assert_allclose(o[i], ref, rtol=1e-10, atol=1e-12)
 
 
+@pytest.mark.parametrize("w", [1, 5, 16, 33])
+def test_decode_window_is_the_last_row_of_the_windowed_prefill_mask(w):
+    """The decode window (flash window_size=(w - 1, 0), query at the end of the
+    keys) against the reference's sliding-window mask (adapters/
+    attention_backend.py:81-86: col <= row and col >= row - w + 1) at the last
+    row, through torch's SDPA in float64 with that mask; w >= len gives the
+    unwindowed decode, and identical keys give the mean of the last w values."""
+    rng = np.random.default_rng(100 + w)
+    B, Hq, Hkv, D = 16, 8, 2, 32
+    lens = [1, 4, 16, 17, 40, 100]
+    q, kp, vp, tables = _random_paged(rng, len(lens), Hq, Hkv, D, B, lens, 64)
+    o = paged_decode_f64(q, kp, vp, tables, lens, B, window_size=w)
+    G = Hq // Hkv
+    for i, n in enumerate(lens):
+        pk, pv, _, _ = gather_packed_kv(kp, vp, [tables[i]], [n], B)
+        row = torch.arange(n)
+        col = torch.arange(n)
+        mask = (col <= row.unsqueeze(1)) & (col >= (row - w + 1).unsqueeze(1))
+        am = torch.where(mask[-1], 0.0, float("-inf")).to(torch.float64).view(1, 1, 1, n)
+        kt = torch.from_numpy(np.repeat(pk, G, axis=1)).permute(1, 0, 2).unsqueeze(0)
+        vt = torch.from_numpy(np.repeat(pv, G, axis=1)).permute(1, 0, 2).unsqueeze(0)
+        qt = torch.from_numpy(q[i]).unsqueeze(0).unsqueeze(2)
+        ref = F.scaled_dot_product_attention(qt, kt, vt, attn_mask=am).squeeze(0).squeeze(1).numpy()
+        np.testing.assert_allclose(o[i], ref, rtol=1e-10, atol=1e-12)
+    full = paged_decode_f64(q, kp, vp, tables, lens, B)
+    np.testing.assert_array_equal(paged_decode_f64(q, kp, vp, tables, lens, B, window_size=100), full)
+    for i, n in enumerate(lens):
+        if n <= w:
+            np.testing.assert_array_equal(o[i], full[i])
+    kc = np.broadcast_to(kp[:1, :1], kp.shape).copy()
+    oc = paged_decode_f64(q, kc, vp, tables, lens, B, window_size=w)
+    for i, n in enumerate(lens):
+        pk, pv, _, _ = gather_packed_kv(kc, vp, [tables[i]], [n], B)
+        mean = pv[max(0, n - w):].mean(axis=0)  # [Hkv, D]
+        np.testing.assert_allclose(oc[i], np.repeat(mean, G, axis=0), rtol=1e-10, atol=1e-12)
+
+
 def test_reference_cpu_path_matches_f64():
     rng = np.random.default_rng(7)
     B, Hq, Hkv, D = 16, 8, 2, 64

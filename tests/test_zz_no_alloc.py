@@ -23,7 +23,7 @@ def _call(lib, fn, b, out, *, layout, dtype_code, chunk=0, ws=None):
     Hkv = b.k_pool.shape[2]
     args = [layout, ptr(b.q), ptr(b.k_store), ptr(b.v_store), ptr(b.block_tables), b.block_tables.shape[1],
             None, ptr(b.seq_lens), None, b.k_store.shape[0], ptr(out), N, Hq, Hkv, D, b.block_size,
-            b.max_seqlen, b.scale, dtype_code, chunk]
+            b.max_seqlen, 0, b.scale, dtype_code, chunk]
     if fn == "mentat_paged_decode":
         args += [ptr(ws), ws.numel()]
     args.append(stream_handle(b.q.device))
@@ -35,7 +35,7 @@ def _both(lib, b, *, layout, dtype_code, chunk=0):
 
     N, Hq, D = b.q.shape
     Hkv = b.k_pool.shape[2]
-    need = lib.mentat_paged_decode_workspace_bytes(layout, N, Hq, Hkv, D, b.block_size, b.max_seqlen, chunk)
+    need = lib.mentat_paged_decode_workspace_bytes(layout, N, Hq, Hkv, D, b.block_size, b.max_seqlen, 0, chunk)
     ws = torch.zeros(max(need, 1), dtype=torch.uint8, device=b.q.device)
     ref = torch.empty_like(b.q)
     got = torch.full_like(b.q, float("nan"))
@@ -85,11 +85,11 @@ def test_noalloc_refuses_sizes_past_the_scratch(gpu):
     lib = get_lib()
     print("case noalloc size limit", flush=True)
     # 4096 sequences x 8 kv heads of native split units need ~70 MB of partial slots
-    assert lib.mentat_paged_decode_workspace_bytes(LAYOUT_NATIVE, 4096, 32, 8, 128, 16, 4096, 0) > 8388608
+    assert lib.mentat_paged_decode_workspace_bytes(LAYOUT_NATIVE, 4096, 32, 8, 128, 16, 4096, 0, 0) > 8388608
     # refused on the size alone: the small buffers below are never read
     t = torch.zeros(64, dtype=torch.int32, device=gpu)
     p = t.data_ptr()
     st = lib.mentat_paged_decode_noalloc(LAYOUT_NATIVE, p, p, p, p, 4, None, p, None, 1, p, 4096, 32, 8,
-                                         128, 16, 4096, 0.088, 2, 0, stream_handle(gpu))
+                                         128, 16, 4096, 0, 0.088, 2, 0, stream_handle(gpu))
     assert st == MENTAT_ESPACE
     torch.cuda.synchronize()
