@@ -176,11 +176,12 @@ int mentat_tree_decode(const void* q, const void* k_store, const void* v_store, 
  * Replaces adapters/attention_backend.py:175-189 attn_prefill (and its SDPA
  * path :43-96 / flash_attn_func(causal=True, window_size=...)).
  * q [batch, seqlen, Hq, D], k/v [batch, seqlen, Hkv, D], out [batch, seqlen,
- * Hq, D], all contiguous, bf16 or f16 (dtype), D in {64, 128}, Hq/Hkv in
- * {1, 2, 4, 8, 16}. Query head h reads kv head h / (Hq/Hkv). Position i
- * attends to keys max(0, i - window + 1) .. i when 0 < window < seqlen, to
- * 0 .. i otherwise. scale: softmax scale (the reference uses D^-1/2).
- * No workspace.
+ * Hq, D], all contiguous, D in {64, 128}; bf16 or f16 with Hq/Hkv in
+ * {1, 2, 4, 8, 16} (MFMA kernel), or fp32 with Hq/Hkv in {1, 2, 4, 8} (VALU
+ * kernel, one query per position). Query head h reads kv head h / (Hq/Hkv).
+ * Position i attends to keys max(0, i - window + 1) .. i when
+ * 0 < window < seqlen, to 0 .. i otherwise. scale: softmax scale (the
+ * reference uses D^-1/2). No workspace.
  * ---------------------------------------------------------------------- */
 int mentat_prefill_attention(const void* q, const void* k, const void* v, void* out, int batch, int seqlen,
                              int Hq, int Hkv, int D, int window, float scale, int dtype, void* stream);

@@ -13,8 +13,9 @@ in place; given packed tensors (the reference's varlen layout) it reads those.
 There is no fallback: without the library or a HIP device it raises.
 
 ``attn_prefill`` (causal attention over a batch of prompts) runs the HIP
-prefill kernel (``mentat_prefill_attention``: MFMA, GQA, sliding window) for
-bf16/f16 inputs; fp32 inputs (the fp32 plumbing model) use torch's device
+prefill kernels (``mentat_prefill_attention``: GQA, sliding window; MFMA for
+bf16/f16, the VALU decode kernel with one query per position for fp32); only
+shapes no kernel takes (head_dim other than 64/128) use torch's device
 matmuls in fp32.
 """
 from __future__ import annotations
@@ -43,12 +44,13 @@ def attn_prefill(
     Position i attends to positions max(0, i - window_size + 1) .. i, as the
     reference's SDPA path does (adapters/attention_backend.py:43-96). K/V may
     have fewer heads than Q (GQA: query head h reads kv head h // (Hq/Hkv)).
-    bf16/f16 (head_dim 64/128): the HIP kernel; otherwise torch matmuls in fp32.
+    head_dim 64/128: the HIP kernels (MFMA for bf16/f16, VALU for fp32); other
+    shapes (no kernel) run torch's device matmuls in fp32.
     """
     B, S, Hq, D = q.shape
     Hkv = k.shape[2]
     G = Hq // Hkv
-    if q.dtype in (torch.bfloat16, torch.float16) and D in (64, 128) and G in (1, 2, 4, 8, 16):
+    if q.dtype in ops.PREFILL_GROUPS and D in (64, 128) and Hq % Hkv == 0 and G in ops.PREFILL_GROUPS[q.dtype]:
         return ops.prefill_attention(q, k, v, window_size=window_size)
     out_dtype = q.dtype
     qf = q.float().permute(0, 2, 1, 3).contiguous()                     # B, Hq, S, D

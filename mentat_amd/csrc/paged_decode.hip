@@ -28,6 +28,13 @@
 // flash_attn_varlen_func(causal=True, window_size=(window - 1, 0)) does for one
 // query aligned to the end of its keys (adapters/attention_backend.py:219-228).
 // The chunks start at the window's first token.
+//
+// Causal prefill (causal_S > 0, packed mode, fp32 prompts): query n of the
+// [B*S, Hq, D] batch is position i = n % S of prompt b = n / S and attends to
+// the keys [b*S, b*S + i] of the [B*S, Hkv, D] K/V (with the window: the last
+// `window` of them), which is the reference's causal prefill attention
+// (adapters/attention_backend.py:43-96) restated as one decode query per
+// position.
 #include <mutex>
 
 #include "mentat_common.h"
@@ -49,6 +56,7 @@ struct DecodeParams {
   float* ws_ml;   // [N, Hq, max_chunks, 2]
   int N, Hq, Hkv, block_size, chunk_tokens, max_chunks;
   int window;        // attend to the last `window` tokens; 0 = all of them
+  int causal_S;      // > 0: packed causal prefill of prompts of causal_S tokens (no cu)
   float scale_log2;  // softmax scale * log2(e)
 };
 
@@ -82,6 +90,9 @@ __global__ __launch_bounds__(kWavesPerBlock * 64) void paged_decode_kernel(Decod
   if constexpr (PAGED) {
     row = p.rows ? p.rows[seq] : seq;
     len = p.lens[row];
+  } else if (p.causal_S > 0) {
+    base_tok = seq - seq % p.causal_S;
+    len = seq % p.causal_S + 1;
   } else {
     base_tok = p.cu[seq];
     len = p.cu[seq + 1] - base_tok;
@@ -212,6 +223,8 @@ __global__ __launch_bounds__(64) void decode_combine_kernel(DecodeParams p) {
   if constexpr (PAGED) {
     const int row = p.rows ? p.rows[seq] : seq;
     len = p.lens[row];
+  } else if (p.causal_S > 0) {
+    len = seq % p.causal_S + 1;
   } else {
     len = p.cu[seq + 1] - p.cu[seq];
   }
@@ -352,7 +365,7 @@ extern "C" int mentat_paged_decode(int layout, const void* q, const void* k_cach
   p.q = q; p.k = k_cache; p.v = v_cache;
   p.tables = block_tables; p.table_stride = table_stride; p.rows = seq_rows; p.lens = seq_lens;
   p.cu = cu_seqlens_k; p.num_blocks = num_blocks; p.out = out;
-  p.N = N; p.Hq = Hq; p.Hkv = Hkv; p.block_size = block_size; p.window = window_size;
+  p.N = N; p.Hq = Hq; p.Hkv = Hkv; p.block_size = block_size; p.window = window_size; p.causal_S = 0;
   p.chunk_tokens = chunk_tokens > 0 ? chunk_tokens : auto_chunk(N, Hkv, block_size, ms);
   p.max_chunks = ceil_div(ms, p.chunk_tokens);
   p.scale_log2 = scale * kLog2e;
@@ -372,6 +385,27 @@ extern "C" int mentat_paged_decode(int layout, const void* q, const void* k_cach
     default: return MENTAT_EUNSUP;
   }
 }
+
+namespace mentat {
+
+// Causal fp32 prefill over [batch, S] prompts on the decode kernel's packed
+// mode: one query per position, one chunk per query (no workspace).
+int causal_prefill_f32(const void* q, const void* k, const void* v, void* out, int batch, int S, int Hq, int Hkv,
+                       int D, int window, float scale, hipStream_t stream) {
+  const long n = (long)batch * S;
+  if (n * Hkv > 0x7fffffffL || (long)S * Hkv * D > 0x7fffffffL) return MENTAT_EUNSUP;
+  DecodeParams p;
+  p.q = q; p.k = k; p.v = v;
+  p.tables = nullptr; p.table_stride = 0; p.rows = nullptr; p.lens = nullptr;
+  p.cu = nullptr; p.num_blocks = 0; p.out = out;
+  p.N = (int)n; p.Hq = Hq; p.Hkv = Hkv; p.block_size = 0; p.window = window; p.causal_S = S;
+  p.chunk_tokens = S; p.max_chunks = 1;
+  p.scale_log2 = scale * kLog2e;
+  p.ws_acc = nullptr; p.ws_ml = nullptr;
+  return dispatch_d<F32, false>(D, Hq / Hkv, p, stream);
+}
+
+}  // namespace mentat
 
 // ---- the allocation-free variant ----------------------------------------------------------
 // mentat_paged_decode_noalloc runs mentat_paged_decode with its workspace in this

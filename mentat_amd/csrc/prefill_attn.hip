@@ -24,6 +24,9 @@
 // 64-key stages measured fastest (more tiles per wavefront raise register use
 // to one wavefront per SIMD; 4 wavefronts or 32-key stages re-stage K/V for
 // fewer rows; 128-key stages halve the resident workgroups).
+//
+// fp32 prompts run on the VALU decode kernel instead (causal_prefill_f32 in
+// paged_decode.hip): one query per position over its visible keys.
 #include "mentat_common.h"
 
 namespace mentat {
@@ -346,6 +349,9 @@ int prefill_d(int D, int G, const PrefillParams& p, int batch, hipStream_t s) {
 
 }  // namespace
 
+int causal_prefill_f32(const void* q, const void* k, const void* v, void* out, int batch, int S, int Hq, int Hkv,
+                       int D, int window, float scale, hipStream_t stream);
+
 }  // namespace mentat
 
 using namespace mentat;
@@ -366,6 +372,7 @@ extern "C" int mentat_prefill_attention(const void* q, const void* k, const void
   switch (dtype) {
     case MENTAT_BF16: return prefill_d<BF16>(D, G, p, batch, s);
     case MENTAT_F16: return prefill_d<F16>(D, G, p, batch, s);
+    case MENTAT_F32: return causal_prefill_f32(q, k, v, out, batch, seqlen, Hq, Hkv, D, p.window, scale, s);
     default: return MENTAT_EUNSUP;
   }
 }

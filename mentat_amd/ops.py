@@ -187,6 +187,10 @@ def paged_decode(
     return out
 
 
+# query heads per kv head that the prefill kernels take, per dtype
+PREFILL_GROUPS = {torch.bfloat16: (1, 2, 4, 8, 16), torch.float16: (1, 2, 4, 8, 16), torch.float32: (1, 2, 4, 8)}
+
+
 def prefill_attention(
     q: torch.Tensor,
     k: torch.Tensor,
@@ -198,8 +202,9 @@ def prefill_attention(
 ) -> torch.Tensor:
     """Causal (optionally sliding-window) GQA attention over a batch of prompts.
 
-    q [B, S, Hq, D], k/v [B, S, Hkv, D] (bf16 or f16, D in {64, 128},
-    Hq/Hkv in {1, 2, 4, 8, 16}); position i attends to keys
+    q [B, S, Hq, D], k/v [B, S, Hkv, D] (D in {64, 128}; bf16 or f16 with
+    Hq/Hkv in {1, 2, 4, 8, 16} on the MFMA kernel, fp32 with Hq/Hkv in
+    {1, 2, 4, 8} on the VALU kernel); position i attends to keys
     max(0, i - window_size + 1) .. i (all of 0 .. i when window_size is None
     or >= S), softmax scale D^-1/2 by default. Returns [B, S, Hq, D].
     """
@@ -210,11 +215,11 @@ def prefill_attention(
     Hkv = k.shape[2]
     dev = q.device
     _require(dev.type == "cuda", "prefill_attention runs on the GPU only (q is on the CPU)")
-    _require(q.dtype in (torch.bfloat16, torch.float16), f"prefill_attention needs bf16/f16, got {q.dtype}")
+    _require(q.dtype in PREFILL_GROUPS, f"prefill_attention needs bf16/f16/fp32, got {q.dtype}")
     _require(k.dtype == q.dtype and v.dtype == q.dtype, "q/k/v dtypes differ")
     _require(k.device == dev and v.device == dev, "q/k/v devices differ")
     _require(D in (64, 128), f"head_dim {D} not supported (64, 128)")
-    _require(Hq % Hkv == 0 and Hq // Hkv in (1, 2, 4, 8, 16), f"Hq/Hkv = {Hq}/{Hkv} not supported")
+    _require(Hq % Hkv == 0 and Hq // Hkv in PREFILL_GROUPS[q.dtype], f"Hq/Hkv = {Hq}/{Hkv} not supported")
     q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
     if out is None:
         out = torch.empty_like(q)

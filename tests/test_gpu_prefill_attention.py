@@ -65,6 +65,34 @@ def test_prefill_matches_float64_reference(gpu, dtype, B, S, Hq, Hkv, D, window)
     assert bool((err <= 2e-2 + 1e-2 * want.abs()).all()), float(err.max())
 
 
+F32_CASES = [c for c in CASES if c[2] // c[3] in (1, 2, 4, 8)] + [
+    (3, 41, 4, 2, 64, None),   # the fp32 plumbing model's heads
+    (2, 300, 4, 2, 64, 33),
+]
+
+
+@pytest.mark.parametrize("B,S,Hq,Hkv,D,window", F32_CASES)
+def test_prefill_f32_matches_float64_reference(gpu, B, S, Hq, Hkv, D, window):
+    """fp32 prompts run on the VALU decode kernel, one query per position
+    (fp32 throughout): |got - want| <= 1e-4 + 1e-4 |want|. attn_prefill
+    routes fp32 to it."""
+    from mentat_amd import ops
+    from mentat_amd.adapters.attention_backend import attn_prefill
+
+    print(f"case prefill f32 B={B} S={S} Hq={Hq} Hkv={Hkv} D={D} window={window}", flush=True)
+    g = torch.Generator().manual_seed(S * 17 + Hq)
+    q = torch.randn(B, S, Hq, D, generator=g)
+    k = torch.randn(B, S, Hkv, D, generator=g)
+    v = torch.randn(B, S, Hkv, D, generator=g)
+    got = ops.prefill_attention(q.cuda(), k.cuda(), v.cuda(), window_size=window)
+    via = attn_prefill(q.cuda(), k.cuda(), v.cuda(), window_size=window)
+    torch.cuda.synchronize()
+    assert torch.equal(got, via)
+    want = _ref(q, k, v, window)
+    err = (got.double().cpu() - want).abs()
+    assert bool((err <= 1e-4 + 1e-4 * want.abs()).all()), float(err.max())
+
+
 def test_prefill_known_answers(gpu):
     from mentat_amd import ops
 
@@ -76,7 +104,19 @@ def test_prefill_known_answers(gpu):
     v = torch.randn(3, 1, 2, 128, dtype=torch.bfloat16, device="cuda")
     o = ops.prefill_attention(q, k, v)
     assert torch.equal(o, v.repeat_interleave(4, dim=2))
+    o = ops.prefill_attention(q.float(), k.float(), v.float())
+    assert torch.equal(o, v.float().repeat_interleave(4, dim=2))
     # identical keys: position i outputs the mean of V over keys max(0, i-w+1) .. i
+    q = torch.randn(2, 40, 4, 64, device="cuda")
+    k = torch.randn(2, 1, 2, 64, device="cuda").expand(2, 40, 2, 64).contiguous()
+    v = torch.randn(2, 40, 2, 64, device="cuda")
+    for w in (None, 3):
+        o = ops.prefill_attention(q, k, v, window_size=w).double().cpu()
+        vf = v.double().cpu()
+        for i in range(40):
+            lo = 0 if w is None else max(0, i - w + 1)
+            mean = vf[:, lo:i + 1].mean(1).repeat_interleave(2, dim=1)
+            assert (o[:, i] - mean).abs().max() < 1e-5, (w, i)
     S = 70
     for w in (None, 5):
         q = torch.randn(1, S, 4, 64, dtype=torch.float16, device="cuda")
