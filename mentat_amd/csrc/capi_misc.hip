@@ -1,7 +1,7 @@
 // Library-level entry points of libmentat_hip.so (version and device queries).
 #include "mentat_common.h"
 
-extern "C" int mentat_abi_version(void) { return 5; }
+extern "C" int mentat_abi_version(void) { return 6; }
 
 extern "C" int mentat_device_count(void) {
   int n = 0;

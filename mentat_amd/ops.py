@@ -573,6 +573,86 @@ def philox4x32_10(counters: torch.Tensor, keys: torch.Tensor) -> torch.Tensor:
     return out
 
 
+def group_plan_device(plan, device, max_segs: Optional[int] = None):
+    """(segs [max_segs, 4], n_segs [1], seg_off, seg_list) as int32 device
+    tensors for :func:`paged_decode_grouped` (uploaded once per plan)."""
+    S = plan.n_segs if max_segs is None else int(max_segs)
+    _require(plan.n_segs <= S, "the plan has more segments than max_segs")
+    segs = np.zeros((max(S, 1), 4), dtype=np.int32)
+    segs[:plan.n_segs] = plan.segs
+    host = np.concatenate([np.array([plan.n_segs], np.int32), segs.reshape(-1), plan.seg_off,
+                           plan.seg_list if plan.seg_list.size else np.zeros(1, np.int32)])
+    buf = torch.from_numpy(host).to(device)
+    a = 1 + segs.size
+    b = a + plan.seg_off.size
+    return buf[1:a].view(-1, 4), buf[0:1], buf[a:b], buf[b:]
+
+
+def paged_decode_grouped(
+    q: torch.Tensor,
+    k_store: torch.Tensor,
+    v_store: torch.Tensor,
+    *,
+    block_tables: torch.Tensor,
+    seq_lens: torch.Tensor,
+    segs: torch.Tensor,
+    n_segs: torch.Tensor,
+    seg_off: torch.Tensor,
+    seg_list: torch.Tensor,
+    scale: Optional[float] = None,
+    out: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """Decode attention over native stores for a batch whose sequences share
+    pages (mentat_paged_decode_grouped): the same result as :func:`paged_decode`,
+    with each shared page read once per group of up to 16 / G queries.
+
+    The plan's device arrays come from :func:`group_plan_device` (or a staging
+    buffer holding the same layout); ``segs`` has max_segs rows, ``n_segs`` is
+    a one-element device tensor. The plan must have been validated on the host
+    (:meth:`mentat_amd.group_plan.GroupPlan.validate`) against these tables.
+    """
+    _require(q.dim() == 3, f"q must be [N, Hq, D], got {tuple(q.shape)}")
+    N, Hq, D = q.shape
+    dev = q.device
+    _require(dev.type == "cuda", "paged_decode_grouped runs on the GPU only")
+    _require(q.dtype in (torch.bfloat16, torch.float16), "paged_decode_grouped needs a 16-bit dtype")
+    _require(k_store.dtype == q.dtype and v_store.dtype == q.dtype, "q/k/v dtypes differ")
+    _require(q.is_contiguous() and k_store.is_contiguous() and v_store.is_contiguous(),
+             "q and the stores must be contiguous")
+    _require(k_store.dim() == 4, "native K store must be [num_blocks, Hkv, block_size, D]")
+    num_blocks, Hkv, block_size, Dk = k_store.shape
+    _require(tuple(v_store.shape) == (num_blocks, Hkv, Dk, block_size),
+             "native V store must be [num_blocks, Hkv, D, block_size]")
+    _require(Dk == D, f"head_dim mismatch q {D} vs cache {Dk}")
+    _require(Hq % Hkv == 0 and Hq // Hkv in (1, 2, 4, 8), "Hq/Hkv must be 1, 2, 4 or 8")
+    _require(block_tables.dim() == 2 and block_tables.stride(1) == 1, "block_tables must be [rows, stride]")
+    for t, name in ((block_tables, "block_tables"), (seq_lens, "seq_lens"), (segs, "segs"),
+                    (n_segs, "n_segs"), (seg_off, "seg_off"), (seg_list, "seg_list")):
+        _check_i32(t, name, dev)
+    _require(segs.dim() == 2 and segs.shape[1] == 4 and segs.is_contiguous(), "segs must be [max_segs, 4]")
+    _require(seg_off.numel() == N + 1, "seg_off must have N + 1 entries")
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    if out is None:
+        out = torch.empty_like(q)
+    else:
+        _require(out.shape == q.shape and out.dtype == q.dtype and out.is_contiguous(), "bad out")
+    if N == 0:
+        return out
+    lib = get_lib()
+    max_segs = segs.shape[0]
+    nbytes = lib.mentat_paged_decode_grouped_workspace_bytes(max_segs, Hq, Hkv, D)
+    _require(nbytes > 0, "no grouped decode kernel for this head geometry")
+    ws = workspace(dev, nbytes)
+    st = lib.mentat_paged_decode_grouped(
+        ptr(q), ptr(k_store), ptr(v_store), ptr(block_tables), block_tables.stride(0), ptr(seq_lens), num_blocks,
+        ptr(segs), ptr(n_segs), max_segs, ptr(seg_off), ptr(seg_list), ptr(out), N, Hq, Hkv, D, block_size,
+        float(scale), DTYPE_CODES[q.dtype], ptr(ws), nbytes, stream_handle(dev),
+    )
+    check(st, "mentat_paged_decode_grouped")
+    return out
+
+
 def tree_decode(
     q: torch.Tensor,
     k_store: torch.Tensor,
