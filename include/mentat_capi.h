@@ -135,39 +135,6 @@ int mentat_paged_decode_noalloc(int layout, const void* q, const void* k_cache, 
                                 void* stream);
 
 /* ------------------------------------------------------------------------
- * Grouped paged decode: mentat_paged_decode on the native layout for a batch
- * whose sequences share pages (the forks of a branching rollout,
- * core/paged_kv_cache.py:152-170), with every shared page read once per group
- * of up to 16 / (Hq/Hkv) queries instead of once per query. Same semantics
- * (core/paged_kv_cache.py:289-368 + adapters/attention_backend.py:192-229:
- * query i attends to all of its cached tokens; no window).
- *
- * The plan (mentat_amd/group_plan.py) cuts the batch's pages into segments:
- *   segs [max_segs][4] int32: owner table row, first 16-token tile, end tile
- *        (exclusive), m0 | count << 16: the segment's pages are those tiles of
- *        the owner row's table, and queries m0 .. m0 + count - 1 (count <=
- *        16 / (Hq/Hkv)) all hold them;
- *   n_segs: device int32 scalar, the number of segments in use (<= max_segs),
- *        read by the kernel, so a captured launch can take a new plan;
- *   seg_off [N + 1], seg_list: query i's segments are
- *        seg_list[seg_off[i] .. seg_off[i + 1]], together covering each of its
- *        tiles exactly once; a query with no segments gets zeros.
- * seq_lens [rows]: tokens per table row (masks the owner's last tile).
- * Pieces of a query are merged inside the kernel by the last arriving piece
- * (arrival counters in the workspace's reserved prefix, left zero). The plan
- * is trusted: the host validates it (GroupPlan.validate). Native layout only,
- * bf16/f16, Hq/Hkv in {1, 2, 4, 8}, N <= 65535, max_segs <= 4096.
- * ---------------------------------------------------------------------- */
-size_t mentat_paged_decode_grouped_workspace_bytes(int max_segs, int Hq, int Hkv, int D);
-
-int mentat_paged_decode_grouped(const void* q, const void* k_store, const void* v_store,
-                                const int32_t* block_tables, int64_t table_stride, const int32_t* seq_lens,
-                                int64_t num_blocks, const int32_t* segs, const int32_t* n_segs, int max_segs,
-                                const int32_t* seg_off, const int32_t* seg_list, void* out, int N, int Hq,
-                                int Hkv, int D, int block_size, float scale, int dtype, void* workspace,
-                                size_t workspace_bytes, void* stream);
-
-/* ------------------------------------------------------------------------
  * Prefix-tree decode attention: the same result as mentat_paged_decode for
  * every query (core/paged_kv_cache.py:289-368 + adapters/attention_backend.py:
  * 192-229: query i attends to all of its cached tokens), computed so that a
@@ -201,6 +168,21 @@ int mentat_tree_decode(const void* q, const void* k_store, const void* v_store, 
                        const int32_t* members, const int32_t* q_slot_offsets, const int32_t* q_slots, int n_slots,
                        void* out, int Nq, int Hq, int Hkv, int D, int block_size, float scale, int dtype,
                        void* workspace, size_t workspace_bytes, void* stream);
+
+/* mentat_tree_decode with the plan's item counts in device memory, so that a
+ * captured launch (a rollout's decode step replayed as a HIP graph) takes a new
+ * plan each step: counts = device int32 [n_shared, n_solo], at most
+ * max_shared / max_solo, the capacities the items, members and q_slots arrays
+ * and the workspace (mentat_tree_decode_workspace_bytes(max_slots, ...)) were
+ * sized for; q_slot_offsets [Nq * Hkv + 1] is read from device memory too. The
+ * kernel runs a fixed grid whose workgroups stride over the items. Same
+ * result as mentat_tree_decode with n_shared / n_solo = the counts. */
+int mentat_tree_decode_counted(const void* q, const void* k_store, const void* v_store,
+                               const int32_t* block_tables, int64_t table_stride, int64_t num_blocks,
+                               const int32_t* items, const int32_t* counts, int max_shared, int max_solo,
+                               const int32_t* members, const int32_t* q_slot_offsets, const int32_t* q_slots,
+                               int max_slots, void* out, int Nq, int Hq, int Hkv, int D, int block_size,
+                               float scale, int dtype, void* workspace, size_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------------
  * Prefill attention: causal (optionally sliding-window) attention over one

@@ -76,15 +76,13 @@ SIGNATURES: dict[str, tuple] = {
             _c_void_p, _c_size, _c_void_p,  # workspace, workspace_bytes, stream
         ],
     ),
-    "mentat_paged_decode_grouped_workspace_bytes": (_c_size, [_c_int] * 4),
-    "mentat_paged_decode_grouped": (
+    "mentat_tree_decode_counted": (
         _c_int,
         [
             _c_void_p, _c_void_p, _c_void_p, _c_void_p,  # q, k_store, v_store, block_tables
-            _c_i64, _c_void_p, _c_i64,  # table_stride, seq_lens, num_blocks
-            _c_void_p, _c_void_p, _c_int, _c_void_p, _c_void_p,  # segs, n_segs, max_segs, seg_off, seg_list
-            _c_void_p, _c_int, _c_int, _c_int, _c_int, _c_int,  # out, N, Hq, Hkv, D, block_size
-            _c_float, _c_int,  # scale, dtype
+            _c_i64, _c_i64, _c_void_p, _c_void_p, _c_int, _c_int,  # table_stride, num_blocks, items, counts, caps
+            _c_void_p, _c_void_p, _c_void_p, _c_int, _c_void_p,  # members, q_slot_offsets, q_slots, max_slots, out
+            _c_int, _c_int, _c_int, _c_int, _c_int, _c_float, _c_int,  # Nq, Hq, Hkv, D, block_size, scale, dtype
             _c_void_p, _c_size, _c_void_p,  # workspace, workspace_bytes, stream
         ],
     ),

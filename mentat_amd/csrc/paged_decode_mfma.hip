@@ -94,14 +94,6 @@ struct NativeParams {
   int TW;            // kv heads per head unit: 4 (a workgroup's waves share tiles) or 1
   int window;        // attend to the last `window` tokens; 0 = all of them
   float scale_log2;
-  int cols;          // query columns per partial slot: G, or 16 for groups
-  long slots;        // partial slots the workspace holds
-  // Groups of sequences sharing pages (grouped mode only):
-  const int32_t* segs;      // [nseg][4]: owner table row, first tile, end tile, m0 | count << 16
-  const int32_t* seg_off;   // [N + 1]: query i's segments are seg_list[seg_off[i] .. seg_off[i + 1])
-  const int32_t* seg_list;
-  const int32_t* nseg_ptr;  // device scalar: the number of segments (clamped to max_segs)
-  int max_segs;             // rows of segs
 };
 
 constexpr int kNativeMaxN = 4096;   // sequences per call (prefix table lives in LDS)
@@ -121,26 +113,20 @@ __device__ __forceinline__ int window_lo(int n, int window) { return window > 0 
 // attended token to the tile of its last.
 __device__ __forceinline__ int tiles_of(int n, int window) { return ((n + 15) >> 4) - (window_lo(n, window) >> 4); }
 
-// Tile prefix over the n work items (sequences, or segments in grouped mode)
-// into s_prefix[0..n]: wave 0 scans 64 items at a time with DPP prefix sums;
-// one barrier publishes it.
-template <bool GRP>
-__device__ void tile_prefix(const NativeParams& p, int32_t* s_prefix, int n) {
+// Tile prefix over the N sequences into s_prefix[0..N]: wave 0 scans 64
+// sequences at a time with DPP prefix sums; one barrier publishes it.
+__device__ void tile_prefix(const NativeParams& p, int32_t* s_prefix) {
   if (threadIdx.x < 64) {
     const int lane = threadIdx.x;
     uint32_t carry = 0;
-    for (int b = 0; b < n; b += 64) {
+    for (int b = 0; b < p.N; b += 64) {
       const int s = b + lane;
-      uint32_t t = 0;
-      if (s < n) {
-        if constexpr (GRP) t = (uint32_t)max(p.segs[4 * s + 2] - p.segs[4 * s + 1], 0);
-        else t = (uint32_t)tiles_of(seq_len_of(p, s), p.window);
-      }
+      const uint32_t t = s < p.N ? (uint32_t)tiles_of(seq_len_of(p, s), p.window) : 0u;
       const uint32_t inc = wave_incl_scan_u32(t) + carry;
-      if (s < n) s_prefix[s] = (int32_t)(inc - t);
+      if (s < p.N) s_prefix[s] = (int32_t)(inc - t);
       carry = (uint32_t)__builtin_amdgcn_readlane((int)inc, 63);
     }
-    if (lane == 0) s_prefix[n] = (int32_t)carry;
+    if (lane == 0) s_prefix[p.N] = (int32_t)carry;
   }
   __syncthreads();
 }
@@ -187,8 +173,8 @@ template <int D>
 __device__ __forceinline__ int partial_col(int pos) {
   return ((pos >> 2) & 15) + 16 * (4 * (pos >> 6) + (pos & 3));
 }
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t partial_rsrc(const NativeParams& p, int D) {
-  const long bytes = p.slots * p.cols * D * (long)sizeof(float);
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t partial_rsrc(const NativeParams& p, int G, int D) {
+  const long bytes = ((long)p.N * p.Hkv + p.W) * G * D * (long)sizeof(float);
   return make_rsrc(p.ws_o, (int)(bytes < 0x7fffffffL ? bytes : 0x7fffffffL));
 }
 
@@ -206,7 +192,7 @@ __device__ __forceinline__ void merge_unit(const NativeParams& p, int seq, int h
   const int g = (lane * E) / D;
   const int d0 = (lane * E) - g * D;
   const int n = w1 - w0 + 1;
-  const __amdgpu_buffer_rsrc_t rw = partial_rsrc(p, D);
+  const __amdgpu_buffer_rsrc_t rw = partial_rsrc(p, G, D);
   float M = kNegInf, L = 0.f, acc[E];
 #pragma unroll
   for (int e = 0; e < E; ++e) acc[e] = 0.f;
@@ -254,90 +240,7 @@ __device__ __forceinline__ void merge_unit(const NativeParams& p, int seq, int h
   for (int e = 0; e < E; ++e) Elem<T>::store1(p.out, ob + partial_col<D>(d0 + e), acc[e] * inv);
 }
 
-// Grouped mode: query qi's output for kv head `head` merges every piece that
-// covered it. For each of its segments s (seg_list order), the pieces are the
-// partial slots (s * HU + hu + e) * TW + wsub of the entities e = w0..w1 that
-// covered the unit (s, hu), at the query columns (qi - m0(s)) * G .. + G - 1 of
-// the slot's 16. The walk over those pieces is held one entry per lane (slot *
-// 16 + first column), 64 entries at a time; lane l owns E = G*D/64 outputs of
-// the query's [G][D] block and the pieces are combined in walk order, as in
-// merge_unit.
-template <typename T, int D, int G>
-__device__ __forceinline__ void merge_query(const NativeParams& p, const int32_t* s_prefix, int qi, int head,
-                                            int hu, int HU, int wsub, int stat, int lane) {
-  constexpr int E = G * D / 64;
-  static_assert(E >= 1, "merge lane split");
-  constexpr int KB = E >= 32 ? 1 : (E >= 16 ? 2 : 4);  // pieces per batch
-  const int g = (lane * E) / D;
-  const int d0 = (lane * E) - g * D;
-  const __amdgpu_buffer_rsrc_t rw = partial_rsrc(p, D);
-  float M = kNegInf, L = 0.f, acc[E];
-#pragma unroll
-  for (int e = 0; e < E; ++e) acc[e] = 0.f;
-  const int j0 = uniform(scalar_load(p.seg_off, qi)), j1 = uniform(scalar_load(p.seg_off, qi + 1));
-  for (int done = 0;; done += 64) {
-    int mine = 0, k = 0;
-    for (int j = j0; j < j1; ++j) {
-      const int sg = uniform(scalar_load(p.seg_list, j));
-      const int m0 = uniform(scalar_load(p.segs, 4L * sg + 3)) & 0xffff;
-      const int pre = uniform(s_prefix[sg]);
-      const int nt = uniform(s_prefix[sg + 1]) - pre;
-      const int ustart = HU * pre + hu * nt;
-      const int w0 = ustart / stat, w1 = (ustart + nt - 1) / stat;
-      const long hunit = (long)sg * HU + hu;
-      for (int e = w0; e <= w1; ++e, ++k)
-        if (k - done == lane) mine = (int)(((hunit + e) * p.TW + wsub) * 16 + (qi - m0) * G);
-    }
-    const int n = min(k - done, 64);
-    for (int k0 = 0; k0 < n; k0 += KB) {
-      float mk[KB], lk[KB], ok[KB][E];
-      // Past-the-end entries of the last batch reload entry n-1 and are dropped.
-      static_for<KB>([&](auto i) {
-        const int ent = __builtin_amdgcn_readlane(mine, min(k0 + (int)i, n - 1));
-        const long slot = ent >> 4;
-        const long col = (ent & 15) + g;
-        mk[i] = get_shared(p.ws_ml + (slot * 16 + col) * 2);
-        lk[i] = get_shared(p.ws_ml + (slot * 16 + col) * 2 + 1);
-        if constexpr (E % 4 == 0) {
-          const int off = (int)(((slot * 16 + col) * D + d0) * (long)sizeof(float));
-#pragma unroll
-          for (int e = 0; e < E; e += 4) {
-            const pd_u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(rw, off + 4 * e, 0, kCoherent);
-#pragma unroll
-            for (int c = 0; c < 4; ++c) ok[i][e + c] = __uint_as_float(v[c]);
-          }
-        } else {
-          const float* wo = p.ws_o + (slot * 16 + col) * D + d0;
-#pragma unroll
-          for (int e = 0; e < E; ++e) ok[i][e] = get_shared(wo + e);
-        }
-      });
-      float Mn = M;
-      static_for<KB>([&](auto i) {
-        if (k0 + (int)i < n) Mn = fmaxf(Mn, mk[i]);
-      });
-      const float ms = (Mn == kNegInf) ? 0.f : Mn;
-      const float cold = (M == kNegInf) ? 0.f : fast_exp2(M - ms);
-      L *= cold;
-#pragma unroll
-      for (int e = 0; e < E; ++e) acc[e] *= cold;
-      static_for<KB>([&](auto i) {
-        const float c = (k0 + (int)i < n && mk[i] != kNegInf) ? fast_exp2(mk[i] - ms) : 0.f;
-        L += lk[i] * c;
-#pragma unroll
-        for (int e = 0; e < E; ++e) acc[e] += ok[i][e] * c;
-      });
-      M = Mn;
-    }
-    if (k - done <= 64) break;
-  }
-  const float inv = L > 0.f ? 1.f / L : 0.f;
-  const long ob = ((long)qi * p.Hq + (long)head * G + g) * D;
-#pragma unroll
-  for (int e = 0; e < E; ++e) Elem<T>::store1(p.out, ob + partial_col<D>(d0 + e), acc[e] * inv);
-}
-
-template <typename T, int D, int G, int B, bool GRP>
+template <typename T, int D, int G, int B>
 __global__ __launch_bounds__(kNativeThreads) void paged_decode_mfma_kernel(NativeParams p) {
   static_assert(D % 32 == 0 && G >= 1 && G <= 16 && B % 16 == 0, "tile shape");
   constexpr int KS = D / 32;  // QK k-steps
@@ -346,14 +249,11 @@ __global__ __launch_bounds__(kNativeThreads) void paged_decode_mfma_kernel(Nativ
   using S = typename T::storage;
 
   __shared__ int32_t s_prefix[kNativeMaxN + 1];
-  // Work items: sequences, or (grouped) segments of pages shared by up to 16 / G
-  // consecutive queries.
-  const int n_items = GRP ? min(max(uniform(scalar_load(p.nseg_ptr, 0)), 0), p.max_segs) : p.N;
-  tile_prefix<GRP>(p, s_prefix, n_items);
+  tile_prefix(p, s_prefix);
 
-  const int TW = p.TW, HU = p.Hkv / TW;              // head units per item
+  const int TW = p.TW, HU = p.Hkv / TW;              // head units per sequence
   const int PE = p.W / TW;                           // partition entities (waves or workgroups)
-  const int T_total = uniform(HU * s_prefix[n_items]);
+  const int T_total = uniform(HU * s_prefix[p.N]);
   // Equal static ranges, one per partition entity. (Claiming a dynamic tail in
   // chunks did not pay: a chunk's first-tile latency and partial publish cost
   // 2-3 us, as much as the spread it was meant to absorb.)
@@ -365,9 +265,7 @@ __global__ __launch_bounds__(kNativeThreads) void paged_decode_mfma_kernel(Nativ
   const int wsub = TW == 1 ? 0 : uniform(threadIdx.x >> 6);  // this wave's head within the unit
   // Sequences without cached tokens get zeros (no tile covers them).
   for (int s = wv; s < p.N; s += p.W) {
-    const bool empty = GRP ? scalar_load(p.seg_off, s + 1) == scalar_load(p.seg_off, s)
-                           : s_prefix[s + 1] == s_prefix[s];
-    if (empty) {
+    if (s_prefix[s + 1] == s_prefix[s]) {
       for (int e = lane; e < p.Hq * D; e += 64) Elem<T>::store1(p.out, (long)s * p.Hq * D + e, 0.f);
     }
   }
@@ -378,7 +276,7 @@ __global__ __launch_bounds__(kNativeThreads) void paged_decode_mfma_kernel(Nativ
   // Unit containing f: last s with HU*prefix[s] <= f (upper_bound - 1).
   int seq;
   {
-    int lo = 0, hi = n_items;
+    int lo = 0, hi = p.N;
     while (lo < hi) {
       const int mid = (lo + hi) >> 1;
       if (HU * s_prefix[mid] <= f) lo = mid + 1; else hi = mid;
@@ -401,33 +299,19 @@ __global__ __launch_bounds__(kNativeThreads) void paged_decode_mfma_kernel(Nativ
     const int ustart = HU * pre + hu * nt;
     const int uend = ustart + nt;
     const int seg_end = min(fend, uend);
-    int row, m0 = seq, cnt = 1, tlo;
-    if constexpr (GRP) {  // the owner's table row, the first tile, the queries m0 .. m0 + cnt - 1
-      row = uniform(scalar_load(p.segs, 4L * seq));
-      tlo = uniform(scalar_load(p.segs, 4L * seq + 1));
-      const int mc = uniform(scalar_load(p.segs, 4L * seq + 3));
-      m0 = mc & 0xffff;
-      cnt = mc >> 16;
-    } else {
-      row = p.rows ? scalar_load(p.rows, seq) : seq;
-    }
+    const int row = p.rows ? scalar_load(p.rows, seq) : seq;
     const int len = max(scalar_load(p.lens, row), 0);
-    const int lo = GRP ? 0 : window_lo(len, p.window);
-    if constexpr (!GRP) tlo = lo >> 4;
-    const int t_first = tile + tlo;  // absolute tile ids within the sequence
+    const int lo = window_lo(len, p.window);
+    const int t_first = tile + (lo >> 4);  // absolute tile ids within the sequence
     const int t_last = t_first + (seg_end - f);
-    const int ncol = GRP ? cnt * G : G;  // valid query columns
     const int32_t* trow = p.tables + (long)row * p.table_stride;
 
-    // Q^T operand: column q = lr holds Q[seq, head*G + q, 32s + 8*lg .. +8]
-    // (grouped: query m0 + lr / G, head head*G + lr % G).
+    // Q^T operand: column q = lr holds Q[seq, head*G + q, 32s + 8*lg .. +8].
     uint4 qo[KS];
-    const int q_seq = GRP ? m0 + lr / G : seq;
-    const int q_head = GRP ? lr % G : lr;
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
-      if (lr < ncol) {
-        const S* qp = (const S*)p.q + ((long)q_seq * p.Hq + (long)head * G + q_head) * D + 32 * s + 8 * lg;
+      if (lr < G) {
+        const S* qp = (const S*)p.q + ((long)seq * p.Hq + (long)head * G + lr) * D + 32 * s + 8 * lg;
         qo[s] = *(const uint4*)qp;
       } else {
         qo[s] = make_uint4(0, 0, 0, 0);
@@ -526,18 +410,15 @@ __global__ __launch_bounds__(kNativeThreads) void paged_decode_mfma_kernel(Nativ
 
     // Emit: O rows (query heads) 4*lg + i, columns d = 16 j + lr.
     const bool whole = (f == ustart) && (seg_end == uend);
-    // Grouped: a query covered by this one piece alone writes its output directly.
-    const bool direct = GRP ? whole && cnt == 1 &&
-                                  scalar_load(p.seg_off, m0 + 1) - scalar_load(p.seg_off, m0) == 1
-                            : whole;
-    if (direct) {
+    const long unit = (long)seq * p.Hkv + head;
+    if (whole) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int qrow = 4 * lg + i;
         const float lq = __shfl(l, qrow);
         if (qrow < G) {
           const float inv = lq > 0.f ? 1.f / lq : 0.f;
-          const long ob = ((long)m0 * p.Hq + (long)head * G + qrow) * D + lr;
+          const long ob = ((long)seq * p.Hq + (long)head * G + qrow) * D + lr;
 #pragma unroll
           for (int j = 0; j < NT; ++j) Elem<T>::store1(p.out, ob + 16 * j, o[j][i] * inv);
         }
@@ -545,13 +426,12 @@ __global__ __launch_bounds__(kNativeThreads) void paged_decode_mfma_kernel(Nativ
     } else {
       const long hunit = (long)seq * HU + hu;
       const long slot = (hunit + pe) * TW + wsub;
-      constexpr int CS = GRP ? 16 : G;  // columns per slot
-      const __amdgpu_buffer_rsrc_t rw = partial_rsrc(p, D);
+      const __amdgpu_buffer_rsrc_t rw = partial_rsrc(p, G, D);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int qrow = 4 * lg + i;
-        if (qrow < ncol) {
-          const int off = (int)(((slot * CS + qrow) * D) * (long)sizeof(float));
+        if (qrow < G) {
+          const int off = (int)(((slot * G + qrow) * D) * (long)sizeof(float));
 #pragma unroll
           for (int j = 0; j < NT; j += 4) {
             const pd_u32x4_t v = {__float_as_uint(o[j][i]), __float_as_uint(o[j + 1][i]),
@@ -560,47 +440,20 @@ __global__ __launch_bounds__(kNativeThreads) void paged_decode_mfma_kernel(Nativ
           }
         }
       }
-      if (lane < ncol) {
-        put_shared(p.ws_ml + (slot * CS + lane) * 2, m);
-        put_shared(p.ws_ml + (slot * CS + lane) * 2 + 1, l);
+      if (lane < G) {
+        put_shared(p.ws_ml + (slot * G + lane) * 2, m);
+        put_shared(p.ws_ml + (slot * G + lane) * 2 + 1, l);
       }
-      // Arrival: the piece's stores complete, then it is counted; the last
-      // piece merges them all.
+      // Arrival: the piece's stores complete, then it is counted; the unit's
+      // last piece merges them all.
+      const int w0 = range_of(ustart), w1 = range_of(uend - 1);  // the ranges that hold the unit's pieces
       __builtin_amdgcn_s_waitcnt(0);
-      if constexpr (!GRP) {
-        const long unit = (long)seq * p.Hkv + head;
-        const int w0 = range_of(ustart), w1 = range_of(uend - 1);  // the ranges that hold the unit's pieces
-        int old = 0;
-        if (lane == 0) old = __hip_atomic_fetch_add(p.ctr + unit, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        old = __shfl(old, 0);
-        if (old == w1 - w0) {
-          merge_unit<T, D, G>(p, seq, head, hunit, wsub, w0, w1, lane);
-          if (lane == 0) __hip_atomic_store(p.ctr + unit, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-      } else {
-        // Lane k counts the piece for query m0 + k, whose pieces are those of
-        // its segments' units (.., hu) over the entities covering each.
-        int old = -1, need = 0;
-        if (lane < cnt) {
-          const int qi = m0 + lane;
-          old = __hip_atomic_fetch_add(p.ctr + (long)qi * p.Hkv + head, 1, __ATOMIC_RELAXED,
-                                       __HIP_MEMORY_SCOPE_AGENT);
-          const int j1 = p.seg_off[qi + 1];
-          for (int j = p.seg_off[qi]; j < j1; ++j) {
-            const int sg = p.seg_list[j];
-            const int spre = s_prefix[sg], snt = s_prefix[sg + 1] - spre;
-            const int us = HU * spre + hu * snt;
-            need += range_of(us + snt - 1) - range_of(us) + 1;
-          }
-        }
-        uint64_t last = __builtin_amdgcn_ballot_w64(lane < cnt && old == need - 1);
-        while (last) {
-          const int k = __builtin_ctzll(last);
-          last &= last - 1;
-          merge_query<T, D, G>(p, s_prefix, m0 + k, head, hu, HU, wsub, stat, lane);
-          if (lane == 0)
-            __hip_atomic_store(p.ctr + (long)(m0 + k) * p.Hkv + head, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
+      int old = 0;
+      if (lane == 0) old = __hip_atomic_fetch_add(p.ctr + unit, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      old = __shfl(old, 0);
+      if (old == w1 - w0) {
+        merge_unit<T, D, G>(p, seq, head, hunit, wsub, w0, w1, lane);
+        if (lane == 0) __hip_atomic_store(p.ctr + unit, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
     }
 
@@ -612,8 +465,8 @@ __global__ __launch_bounds__(kNativeThreads) void paged_decode_mfma_kernel(Nativ
     if (hu == HU) {
       hu = 0;
       ++seq;
-      while (seq < n_items && s_prefix[seq + 1] == s_prefix[seq]) ++seq;
-      if (seq >= n_items) break;
+      while (seq < p.N && s_prefix[seq + 1] == s_prefix[seq]) ++seq;
+      if (seq >= p.N) break;
       seq = uniform(seq);
       pre = uniform(s_prefix[seq]);
       nt = uniform(s_prefix[seq + 1]) - pre;
@@ -624,7 +477,7 @@ __global__ __launch_bounds__(kNativeThreads) void paged_decode_mfma_kernel(Nativ
 
 // Persistent grid size of one kernel instantiation: its resident wavefronts on
 // the current device (CUs x resident workgroups x 4), cached per device.
-template <typename T, int D, int G, int B, bool GRP>
+template <typename T, int D, int G, int B>
 static int persistent_waves() {
   static int cached[64] = {0};
   int dev = 0;
@@ -634,7 +487,7 @@ static int persistent_waves() {
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
     cus = 256;
   int blocks = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, paged_decode_mfma_kernel<T, D, G, B, GRP>,
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, paged_decode_mfma_kernel<T, D, G, B>,
                                                    kNativeThreads, 0) != hipSuccess || blocks <= 0)
     blocks = 1;
   cached[dev] = cus * blocks * (kNativeThreads / 64);
@@ -643,69 +496,63 @@ static int persistent_waves() {
 
 // The largest persistent grid over the instantiations a call with this head
 // geometry may use; the workspace holds one partial slot per wavefront.
-// Grouped instantiations exist for G <= 8 (at least two queries per tile).
-template <int D, int G, bool GRP>
+template <int D, int G>
 static int max_persistent_waves() {
-  return max(max(max(persistent_waves<BF16, D, G, 16, GRP>(), persistent_waves<BF16, D, G, 32, GRP>()),
-                 persistent_waves<BF16, D, G, 64, GRP>()),
-             max(max(persistent_waves<F16, D, G, 16, GRP>(), persistent_waves<F16, D, G, 32, GRP>()),
-                 persistent_waves<F16, D, G, 64, GRP>()));
+  return max(max(max(persistent_waves<BF16, D, G, 16>(), persistent_waves<BF16, D, G, 32>()),
+                 persistent_waves<BF16, D, G, 64>()),
+             max(max(persistent_waves<F16, D, G, 16>(), persistent_waves<F16, D, G, 32>()),
+                 persistent_waves<F16, D, G, 64>()));
 }
-template <bool GRP>
 static int workspace_waves(int D, int G) {
-  if (GRP && G > 8) return 0;
   switch (D * 100 + G) {
-    case 6401: return max_persistent_waves<64, 1, GRP>();
-    case 6402: return max_persistent_waves<64, 2, GRP>();
-    case 6404: return max_persistent_waves<64, 4, GRP>();
-    case 6408: return max_persistent_waves<64, 8, GRP>();
-    case 6416: return GRP ? 0 : max_persistent_waves<64, 16, false>();
-    case 12801: return max_persistent_waves<128, 1, GRP>();
-    case 12802: return max_persistent_waves<128, 2, GRP>();
-    case 12804: return max_persistent_waves<128, 4, GRP>();
-    case 12808: return max_persistent_waves<128, 8, GRP>();
-    case 12816: return GRP ? 0 : max_persistent_waves<128, 16, false>();
+    case 6401: return max_persistent_waves<64, 1>();
+    case 6402: return max_persistent_waves<64, 2>();
+    case 6404: return max_persistent_waves<64, 4>();
+    case 6408: return max_persistent_waves<64, 8>();
+    case 6416: return max_persistent_waves<64, 16>();
+    case 12801: return max_persistent_waves<128, 1>();
+    case 12802: return max_persistent_waves<128, 2>();
+    case 12804: return max_persistent_waves<128, 4>();
+    case 12808: return max_persistent_waves<128, 8>();
+    case 12816: return max_persistent_waves<128, 16>();
     default: return 0;
   }
 }
 
-template <typename T, int D, int G, int B, bool GRP>
+template <typename T, int D, int G, int B>
 static int launch_native(NativeParams p, hipStream_t stream) {
-  p.W = persistent_waves<T, D, G, B, GRP>();  // <= the workspace's wave count
-  hipLaunchKernelGGL((paged_decode_mfma_kernel<T, D, G, B, GRP>), dim3(p.W / 4), dim3(kNativeThreads), 0, stream,
-                     p);
+  p.W = persistent_waves<T, D, G, B>();  // <= the workspace's wave count
+  hipLaunchKernelGGL((paged_decode_mfma_kernel<T, D, G, B>), dim3(p.W / 4), dim3(kNativeThreads), 0, stream, p);
   return (int)hipGetLastError();
 }
 
-template <typename T, int D, int G, bool GRP>
+template <typename T, int D, int G>
 static int native_b(const NativeParams& p, hipStream_t s) {
   switch (p.B) {
-    case 16: return launch_native<T, D, G, 16, GRP>(p, s);
-    case 32: return launch_native<T, D, G, 32, GRP>(p, s);
-    case 64: return launch_native<T, D, G, 64, GRP>(p, s);
+    case 16: return launch_native<T, D, G, 16>(p, s);
+    case 32: return launch_native<T, D, G, 32>(p, s);
+    case 64: return launch_native<T, D, G, 64>(p, s);
     default: return MENTAT_EUNSUP;
   }
 }
 
-template <typename T, int D, bool GRP>
+template <typename T, int D>
 static int native_g(int G, const NativeParams& p, hipStream_t s) {
   switch (G) {
-    case 1: return native_b<T, D, 1, GRP>(p, s);
-    case 2: return native_b<T, D, 2, GRP>(p, s);
-    case 4: return native_b<T, D, 4, GRP>(p, s);
-    case 8: return native_b<T, D, 8, GRP>(p, s);
-    case 16:
-      if constexpr (GRP) return MENTAT_EUNSUP;
-      else return native_b<T, D, 16, false>(p, s);
+    case 1: return native_b<T, D, 1>(p, s);
+    case 2: return native_b<T, D, 2>(p, s);
+    case 4: return native_b<T, D, 4>(p, s);
+    case 8: return native_b<T, D, 8>(p, s);
+    case 16: return native_b<T, D, 16>(p, s);
     default: return MENTAT_EUNSUP;
   }
 }
 
-template <typename T, bool GRP>
+template <typename T>
 static int native_d(int D, int G, const NativeParams& p, hipStream_t s) {
   switch (D) {
-    case 64: return native_g<T, 64, GRP>(G, p, s);
-    case 128: return native_g<T, 128, GRP>(G, p, s);
+    case 64: return native_g<T, 64>(G, p, s);
+    case 128: return native_g<T, 128>(G, p, s);
     default: return MENTAT_EUNSUP;
   }
 }
@@ -718,7 +565,7 @@ using namespace mentat;
 // slots (units + waves).
 size_t native_workspace_bytes(int N, int Hq, int Hkv, int D) {
   const int G = Hq / Hkv;
-  const int W = workspace_waves<false>(D, G);
+  const int W = workspace_waves(D, G);
   const size_t slots = (size_t)N * Hkv + W;
   return kWsReserved + slots * G * (D + 2) * sizeof(float);
 }
@@ -733,76 +580,23 @@ int native_paged_decode(const void* q, const void* k_cache, const void* v_cache,
   if (!block_tables || !seq_lens || table_stride <= 0 || num_blocks <= 0) return MENTAT_EINVAL;
   const size_t need = native_workspace_bytes(N, Hq, Hkv, D);
   if (!workspace || workspace_bytes < need) return MENTAT_ESPACE;
-  NativeParams p = {};
+  NativeParams p;
   p.q = q; p.k = k_cache; p.v = v_cache;
   p.tables = block_tables; p.table_stride = table_stride; p.rows = seq_rows; p.lens = seq_lens;
   p.num_blocks = num_blocks; p.out = out;
   const int G = Hq / Hkv;
-  p.N = N; p.Hq = Hq; p.Hkv = Hkv; p.B = block_size; p.W = workspace_waves<false>(D, G);
+  p.N = N; p.Hq = Hq; p.Hkv = Hkv; p.B = block_size; p.W = workspace_waves(D, G);
   if (p.W <= 0) return MENTAT_EUNSUP;
   p.TW = (Hkv % 4 == 0) ? 4 : 1;
   p.window = window_size;
   p.scale_log2 = scale * kLog2e;
   const size_t slots = (size_t)N * Hkv + p.W;
-  p.cols = G;
-  p.slots = (long)slots;
   p.ctr = (int32_t*)workspace;
   p.ws_o = (float*)((char*)workspace + kWsReserved);
   p.ws_ml = p.ws_o + slots * G * D;
   switch (dtype) {
-    case MENTAT_BF16: return native_d<BF16, false>(D, G, p, stream);
-    case MENTAT_F16: return native_d<F16, false>(D, G, p, stream);
-    default: return MENTAT_EUNSUP;
-  }
-}
-
-// ---- grouped decode: sequences that share pages read them together ----------------------------
-
-extern "C" size_t mentat_paged_decode_grouped_workspace_bytes(int max_segs, int Hq, int Hkv, int D) {
-  if (max_segs < 0 || Hq <= 0 || Hkv <= 0 || D <= 0 || Hq % Hkv) return 0;
-  const int W = workspace_waves<true>(D, Hq / Hkv);
-  if (W <= 0) return 0;
-  const size_t slots = (size_t)max_segs * Hkv + W;
-  return kWsReserved + slots * 16 * (D + 2) * sizeof(float);
-}
-
-extern "C" int mentat_paged_decode_grouped(const void* q, const void* k_store, const void* v_store,
-                                           const int32_t* block_tables, int64_t table_stride,
-                                           const int32_t* seq_lens, int64_t num_blocks, const int32_t* segs,
-                                           const int32_t* n_segs, int max_segs, const int32_t* seg_off,
-                                           const int32_t* seg_list, void* out, int N, int Hq, int Hkv, int D,
-                                           int block_size, float scale, int dtype, void* workspace,
-                                           size_t workspace_bytes, void* stream) {
-  if (N == 0) return MENTAT_OK;
-  if (!q || !k_store || !v_store || !out || !block_tables || !seq_lens || !segs || !n_segs || !seg_off ||
-      !seg_list || N < 0 || Hq <= 0 || Hkv <= 0 || D <= 0 || Hq % Hkv || table_stride <= 0 || num_blocks <= 0 ||
-      max_segs < 0)
-    return MENTAT_EINVAL;
-  const int G = Hq / Hkv;
-  if (G > 8 || N > 0xffff || (long)N * Hkv > kMaxNativeUnits || max_segs > kNativeMaxN) return MENTAT_EUNSUP;
-  if (block_size != 16 && block_size != 32 && block_size != 64) return MENTAT_EUNSUP;
-  const size_t need = mentat_paged_decode_grouped_workspace_bytes(max_segs, Hq, Hkv, D);
-  if (need == 0) return MENTAT_EUNSUP;
-  if (!workspace || workspace_bytes < need) return MENTAT_ESPACE;
-  NativeParams p = {};
-  p.q = q; p.k = k_store; p.v = v_store;
-  p.tables = block_tables; p.table_stride = table_stride; p.rows = nullptr; p.lens = seq_lens;
-  p.num_blocks = num_blocks; p.out = out;
-  p.N = N; p.Hq = Hq; p.Hkv = Hkv; p.B = block_size; p.W = workspace_waves<true>(D, G);
-  p.TW = (Hkv % 4 == 0) ? 4 : 1;
-  p.window = 0;
-  p.scale_log2 = scale * kLog2e;
-  const size_t slots = (size_t)max_segs * Hkv + p.W;
-  if (slots * 16 > 0x7fffffffUL) return MENTAT_EUNSUP;  // piece entries hold slot * 16 in 31 bits
-  p.cols = 16;
-  p.slots = (long)slots;
-  p.ctr = (int32_t*)workspace;
-  p.ws_o = (float*)((char*)workspace + kWsReserved);
-  p.ws_ml = p.ws_o + slots * 16 * D;
-  p.segs = segs; p.seg_off = seg_off; p.seg_list = seg_list; p.nseg_ptr = n_segs; p.max_segs = max_segs;
-  switch (dtype) {
-    case MENTAT_BF16: return native_d<BF16, true>(D, G, p, (hipStream_t)stream);
-    case MENTAT_F16: return native_d<F16, true>(D, G, p, (hipStream_t)stream);
+    case MENTAT_BF16: return native_d<BF16>(D, G, p, stream);
+    case MENTAT_F16: return native_d<F16>(D, G, p, stream);
     default: return MENTAT_EUNSUP;
   }
 }

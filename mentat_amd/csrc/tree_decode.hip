@@ -72,6 +72,8 @@ struct TreeParams {
   int64_t num_blocks;
   const int32_t* items;
   int n_shared, n_solo;
+  const int32_t* counts;  // optional device [n_shared, n_solo] (within the host's capacities above)
+  int grid_shared;        // with counts: workgroups [0, grid_shared) take the shared tasks
   const int32_t* members;
   float* ws_o;         // [slots][G][D]
   float* ws_ml;        // [slots][G][2]
@@ -433,6 +435,24 @@ __global__ __launch_bounds__(kTreeThreads) void tree_decode_kernel(TreeParams p)
   __shared__ uint4 lds_words[4 * TileLds<D>::STAGE / 16];  // 2 stages x 2 tiles
   char* lds = (char*)lds_words;
   const int bid = blockIdx.x;
+  if (p.counts) {
+    // Item counts from device memory (a captured launch takes each step's
+    // plan): a fixed grid, workgroups [0, grid_shared) stride over the shared
+    // tasks, the others' wavefronts over the solo items.
+    const int n_shared = min(max(tld(p.counts, 0), 0), p.n_shared);
+    const int n_solo = min(max(tld(p.counts, 1), 0), p.n_solo);
+    if (bid < p.grid_shared) {
+      for (int t = bid; t < n_shared; t += p.grid_shared) {
+        tree_shared<T, D, G, B>(p, p.items + (long)t * kItemFields, lds);
+        __syncthreads();  // the next task restages the LDS ring
+      }
+      return;
+    }
+    const int step = ((int)gridDim.x - p.grid_shared) * kTreeWaves;
+    for (int it = (bid - p.grid_shared) * kTreeWaves + tuni(threadIdx.x >> 6); it < n_solo; it += step)
+      tree_solo<T, D, G, B>(p, p.items + (long)(n_shared + it) * kItemFields);
+    return;
+  }
   if (bid < p.n_shared) {
     tree_shared<T, D, G, B>(p, p.items + (long)bid * kItemFields, lds);
     return;
@@ -493,9 +513,15 @@ __global__ __launch_bounds__(64) void tree_merge_kernel(TreeParams p) {
   for (int j = 0; j < E; ++j) Elem<T>::store1(p.out, ob + j, acc[j] * inv);
 }
 
+// Fixed grid of the counted mode: workgroups for the shared tasks and for the
+// solo items, each at most what the capacities need.
+constexpr int kTreeGridShared = 256;
+constexpr int kTreeGridSolo = 1024;
+
 template <typename T, int D, int G, int B>
 static int tree_launch(const TreeParams& p, hipStream_t s) {
-  const int blocks = p.n_shared + (p.n_solo + kTreeWaves - 1) / kTreeWaves;
+  const int blocks = p.counts ? p.grid_shared + min(kTreeGridSolo, (p.n_solo + kTreeWaves - 1) / kTreeWaves)
+                              : p.n_shared + (p.n_solo + kTreeWaves - 1) / kTreeWaves;
   if (blocks > 0)
     hipLaunchKernelGGL((tree_decode_kernel<T, D, G, B>), dim3(blocks), dim3(kTreeThreads), 0, s, p);
   hipError_t e = hipGetLastError();
@@ -543,12 +569,12 @@ extern "C" size_t mentat_tree_decode_workspace_bytes(int n_slots, int Hq, int Hk
   return kWsReserved + (size_t)n_slots * G * (D + 2) * sizeof(float);
 }
 
-extern "C" int mentat_tree_decode(const void* q, const void* k_store, const void* v_store, const int32_t* block_tables,
-                                  int64_t table_stride, int64_t num_blocks, const int32_t* items, int n_shared,
-                                  int n_solo, const int32_t* members, const int32_t* q_slot_offsets,
-                                  const int32_t* q_slots, int n_slots, void* out, int Nq, int Hq, int Hkv, int D,
-                                  int block_size, float scale, int dtype, void* workspace, size_t workspace_bytes,
-                                  void* stream) {
+static int tree_decode_call(const void* q, const void* k_store, const void* v_store, const int32_t* block_tables,
+                            int64_t table_stride, int64_t num_blocks, const int32_t* items, int n_shared, int n_solo,
+                            const int32_t* counts, const int32_t* members, const int32_t* q_slot_offsets,
+                            const int32_t* q_slots, int n_slots, void* out, int Nq, int Hq, int Hkv, int D,
+                            int block_size, float scale, int dtype, void* workspace, size_t workspace_bytes,
+                            void* stream) {
   if (Nq == 0) return MENTAT_OK;
   if (!q || !k_store || !v_store || !block_tables || !out || !q_slot_offsets || Nq < 0 || Hq <= 0 || Hkv <= 0 ||
       Hq % Hkv != 0 || table_stride <= 0 || num_blocks <= 0 || n_shared < 0 || n_solo < 0 || n_slots < 0)
@@ -559,6 +585,8 @@ extern "C" int mentat_tree_decode(const void* q, const void* k_store, const void
   TreeParams p;
   p.q = q; p.k = k_store; p.v = v_store; p.tables = block_tables; p.table_stride = table_stride;
   p.num_blocks = num_blocks; p.items = items; p.n_shared = n_shared; p.n_solo = n_solo; p.members = members;
+  p.counts = counts;
+  p.grid_shared = counts ? min(kTreeGridShared, n_shared) : 0;
   const int G = Hq / Hkv;
   p.ws_o = (float*)((char*)workspace + kWsReserved);
   p.ws_ml = p.ws_o + (size_t)n_slots * G * D;
@@ -570,4 +598,28 @@ extern "C" int mentat_tree_decode(const void* q, const void* k_store, const void
     case MENTAT_F16: return tree_d<F16>(D, G, p, s);
     default: return MENTAT_EUNSUP;
   }
+}
+
+extern "C" int mentat_tree_decode(const void* q, const void* k_store, const void* v_store, const int32_t* block_tables,
+                                  int64_t table_stride, int64_t num_blocks, const int32_t* items, int n_shared,
+                                  int n_solo, const int32_t* members, const int32_t* q_slot_offsets,
+                                  const int32_t* q_slots, int n_slots, void* out, int Nq, int Hq, int Hkv, int D,
+                                  int block_size, float scale, int dtype, void* workspace, size_t workspace_bytes,
+                                  void* stream) {
+  return tree_decode_call(q, k_store, v_store, block_tables, table_stride, num_blocks, items, n_shared, n_solo,
+                          nullptr, members, q_slot_offsets, q_slots, n_slots, out, Nq, Hq, Hkv, D, block_size, scale,
+                          dtype, workspace, workspace_bytes, stream);
+}
+
+extern "C" int mentat_tree_decode_counted(const void* q, const void* k_store, const void* v_store,
+                                          const int32_t* block_tables, int64_t table_stride, int64_t num_blocks,
+                                          const int32_t* items, const int32_t* counts, int max_shared, int max_solo,
+                                          const int32_t* members, const int32_t* q_slot_offsets,
+                                          const int32_t* q_slots, int max_slots, void* out, int Nq, int Hq, int Hkv,
+                                          int D, int block_size, float scale, int dtype, void* workspace,
+                                          size_t workspace_bytes, void* stream) {
+  if (!counts) return MENTAT_EINVAL;
+  return tree_decode_call(q, k_store, v_store, block_tables, table_stride, num_blocks, items, max_shared, max_solo,
+                          counts, members, q_slot_offsets, q_slots, max_slots, out, Nq, Hq, Hkv, D, block_size, scale,
+                          dtype, workspace, workspace_bytes, stream);
 }

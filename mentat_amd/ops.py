@@ -573,49 +573,67 @@ def philox4x32_10(counters: torch.Tensor, keys: torch.Tensor) -> torch.Tensor:
     return out
 
 
-def group_plan_device(plan, device, max_segs: Optional[int] = None):
-    """(segs [max_segs, 4], n_segs [1], seg_off, seg_list) as int32 device
-    tensors for :func:`paged_decode_grouped` (uploaded once per plan)."""
-    S = plan.n_segs if max_segs is None else int(max_segs)
-    _require(plan.n_segs <= S, "the plan has more segments than max_segs")
-    segs = np.zeros((max(S, 1), 4), dtype=np.int32)
-    segs[:plan.n_segs] = plan.segs
-    host = np.concatenate([np.array([plan.n_segs], np.int32), segs.reshape(-1), plan.seg_off,
-                           plan.seg_list if plan.seg_list.size else np.zeros(1, np.int32)])
-    buf = torch.from_numpy(host).to(device)
-    a = 1 + segs.size
-    b = a + plan.seg_off.size
-    return buf[1:a].view(-1, 4), buf[0:1], buf[a:b], buf[b:]
+class TreePlanBuffers:
+    """Device arrays of prefix-tree plans with fixed capacities, refilled per
+    call (for launches captured once and replayed with new plans): one int32
+    buffer holding counts [2], items [max_items, 8], members [max_slots],
+    q_slot_offsets [Nq * Hkv + 1], q_slots [max_slots], and a pinned host twin
+    the plan is written into before one copy."""
+
+    def __init__(self, device, Nq: int, Hkv: int, max_shared: int, max_solo: int, max_slots: int):
+        self.Nq, self.Hkv = Nq, Hkv
+        self.max_shared, self.max_solo, self.max_slots = max_shared, max_solo, max_slots
+        mi = max_shared + max_solo
+        self._cuts = np.cumsum([0, 2, 8 * max(mi, 1), max(max_slots, 1), Nq * Hkv + 1, max(max_slots, 1)])
+        n = int(self._cuts[-1])
+        self.host = torch.zeros(n, dtype=torch.int32, pin_memory=True)
+        self.host_np = self.host.numpy()
+        self.dev = torch.zeros(n, dtype=torch.int32, device=device)
+        c = self._cuts
+        self.counts = self.dev[c[0]:c[1]]
+        self.items = self.dev[c[1]:c[2]]
+        self.members = self.dev[c[2]:c[3]]
+        self.q_slot_offsets = self.dev[c[3]:c[4]]
+        self.q_slots = self.dev[c[4]:c[5]]
+
+    def fits(self, plan) -> bool:
+        return plan.n_shared <= self.max_shared and plan.n_solo <= self.max_solo and plan.n_slots <= self.max_slots
+
+    def write(self, plan, n: int) -> None:
+        """Plan of n <= Nq queries into the host twin (queries n .. Nq - 1 get no slots)."""
+        _require(self.fits(plan), "the plan exceeds the buffers' capacities")
+        c, h = self._cuts, self.host_np
+        h[0], h[1] = plan.n_shared, plan.n_solo
+        k = plan.items.size
+        h[c[1]:c[1] + k] = plan.items.reshape(-1)
+        h[c[2]:c[2] + plan.members.size] = plan.members
+        off = h[c[3]:c[4]]
+        off[:n * self.Hkv + 1] = plan.q_slot_offsets
+        off[n * self.Hkv + 1:] = plan.q_slot_offsets[-1]
+        h[c[4]:c[4] + plan.q_slots.size] = plan.q_slots
+
+    def upload(self) -> None:
+        self.dev.copy_(self.host, non_blocking=True)
 
 
-def paged_decode_grouped(
+def tree_decode_counted(
     q: torch.Tensor,
     k_store: torch.Tensor,
     v_store: torch.Tensor,
     *,
     block_tables: torch.Tensor,
-    seq_lens: torch.Tensor,
-    segs: torch.Tensor,
-    n_segs: torch.Tensor,
-    seg_off: torch.Tensor,
-    seg_list: torch.Tensor,
+    bufs: TreePlanBuffers,
     scale: Optional[float] = None,
     out: Optional[torch.Tensor] = None,
 ) -> torch.Tensor:
-    """Decode attention over native stores for a batch whose sequences share
-    pages (mentat_paged_decode_grouped): the same result as :func:`paged_decode`,
-    with each shared page read once per group of up to 16 / G queries.
-
-    The plan's device arrays come from :func:`group_plan_device` (or a staging
-    buffer holding the same layout); ``segs`` has max_segs rows, ``n_segs`` is
-    a one-element device tensor. The plan must have been validated on the host
-    (:meth:`mentat_amd.group_plan.GroupPlan.validate`) against these tables.
-    """
+    """:func:`tree_decode` with the plan in ``bufs`` (device arrays of fixed
+    capacity; mentat_tree_decode_counted reads the item counts on the device).
+    The plan written there must have been validated against these tables."""
     _require(q.dim() == 3, f"q must be [N, Hq, D], got {tuple(q.shape)}")
-    N, Hq, D = q.shape
+    Nq, Hq, D = q.shape
     dev = q.device
-    _require(dev.type == "cuda", "paged_decode_grouped runs on the GPU only")
-    _require(q.dtype in (torch.bfloat16, torch.float16), "paged_decode_grouped needs a 16-bit dtype")
+    _require(dev.type == "cuda", "tree_decode runs on the GPU only")
+    _require(q.dtype in (torch.bfloat16, torch.float16), "tree_decode needs a 16-bit dtype")
     _require(k_store.dtype == q.dtype and v_store.dtype == q.dtype, "q/k/v dtypes differ")
     _require(q.is_contiguous() and k_store.is_contiguous() and v_store.is_contiguous(),
              "q and the stores must be contiguous")
@@ -623,33 +641,26 @@ def paged_decode_grouped(
     num_blocks, Hkv, block_size, Dk = k_store.shape
     _require(tuple(v_store.shape) == (num_blocks, Hkv, Dk, block_size),
              "native V store must be [num_blocks, Hkv, D, block_size]")
-    _require(Dk == D, f"head_dim mismatch q {D} vs cache {Dk}")
-    _require(Hq % Hkv == 0 and Hq // Hkv in (1, 2, 4, 8), "Hq/Hkv must be 1, 2, 4 or 8")
+    _require(Dk == D and Hq % Hkv == 0 and 16 % (Hq // Hkv) == 0, "bad head geometry")
     _require(block_tables.dim() == 2 and block_tables.stride(1) == 1, "block_tables must be [rows, stride]")
-    for t, name in ((block_tables, "block_tables"), (seq_lens, "seq_lens"), (segs, "segs"),
-                    (n_segs, "n_segs"), (seg_off, "seg_off"), (seg_list, "seg_list")):
-        _check_i32(t, name, dev)
-    _require(segs.dim() == 2 and segs.shape[1] == 4 and segs.is_contiguous(), "segs must be [max_segs, 4]")
-    _require(seg_off.numel() == N + 1, "seg_off must have N + 1 entries")
+    _check_i32(block_tables, "block_tables", dev)
+    _require(bufs.Nq == Nq and bufs.Hkv == Hkv, "the plan buffers were sized for another batch")
     if scale is None:
         scale = 1.0 / math.sqrt(D)
     if out is None:
         out = torch.empty_like(q)
-    else:
-        _require(out.shape == q.shape and out.dtype == q.dtype and out.is_contiguous(), "bad out")
-    if N == 0:
+    if Nq == 0:
         return out
     lib = get_lib()
-    max_segs = segs.shape[0]
-    nbytes = lib.mentat_paged_decode_grouped_workspace_bytes(max_segs, Hq, Hkv, D)
-    _require(nbytes > 0, "no grouped decode kernel for this head geometry")
-    ws = workspace(dev, nbytes)
-    st = lib.mentat_paged_decode_grouped(
-        ptr(q), ptr(k_store), ptr(v_store), ptr(block_tables), block_tables.stride(0), ptr(seq_lens), num_blocks,
-        ptr(segs), ptr(n_segs), max_segs, ptr(seg_off), ptr(seg_list), ptr(out), N, Hq, Hkv, D, block_size,
+    nbytes = lib.mentat_tree_decode_workspace_bytes(bufs.max_slots, Hq, Hkv, D)
+    ws = workspace(dev, nbytes) if nbytes else None
+    st = lib.mentat_tree_decode_counted(
+        ptr(q), ptr(k_store), ptr(v_store), ptr(block_tables), block_tables.stride(0), num_blocks,
+        ptr(bufs.items), ptr(bufs.counts), bufs.max_shared, bufs.max_solo, ptr(bufs.members),
+        ptr(bufs.q_slot_offsets), ptr(bufs.q_slots), bufs.max_slots, ptr(out), Nq, Hq, Hkv, D, block_size,
         float(scale), DTYPE_CODES[q.dtype], ptr(ws), nbytes, stream_handle(dev),
     )
-    check(st, "mentat_paged_decode_grouped")
+    check(st, "mentat_tree_decode_counted")
     return out
 
 

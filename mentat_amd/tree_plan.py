@@ -1,13 +1,24 @@
 """Host plan for the prefix-tree decode kernel (mentat_tree_decode).
 
-The decode batch's contexts are split into segments: maximal runs of pages
-that a set of sequences reaches through the same block ids (with the same
-number of valid tokens), i.e. the edges of the prefix tree the batch forms —
-a shared prompt, internal branches, each leaf's private tail. The sharing
-structure is the same in every layer (forks, frees and copy-on-write treat all
-layers alike; only the block ids differ), so a plan is built once per decode
-step from layer 0's tables and reused by every layer: a segment names a
-representative table row and the kernel reads that layer's ids from it.
+The decode batch's contexts are split into segments: runs of pages that a set
+of sequences reaches through the same block ids (with the same number of valid
+tokens), i.e. the edges of the prefix tree the batch forms — a shared prompt,
+internal branches, each leaf's private tail. The sharing structure is the same
+in every layer (forks, frees and copy-on-write treat all layers alike; only
+the block ids differ), so a plan is built once per decode step from layer 0's
+tables and reused by every layer: a segment names a representative table row
+and the kernel reads that layer's ids from it.
+
+Segments come from the common prefixes of neighbours in batch order. A fork
+copies its parent's block ids (core/paged_kv_cache.py:152-170), so two
+sequences share exactly the pages on which their tables agree, and in the
+reference's depth-first leaf order (core/generator_utils.py:171-189) the
+sequences holding a page are consecutive. lcp[i] = the leading pages whose
+ids (and valid token counts) sequence i has in common with sequence i - 1; a
+page p of sequence i is then shared by i .. j exactly when lcp[k] > p for
+i < k <= j, and each sequence's pages past lcp[i] are cut where that run of
+neighbours gets shorter. Any batch order gives a correct plan (pages shared by
+sequences that are not neighbours are read once per run of neighbours).
 
 Work: each segment is cut into chunks of 16-token tiles and each (chunk, kv
 head) gets its members' queries in groups of 16 / G (one MFMA query tile;
@@ -44,6 +55,27 @@ class Segment:
 
 
 @dataclass
+class SegmentArrays:
+    """Segments as int64 arrays: owner table row, first page, end page
+    (exclusive), end token (exclusive, absolute), first query, query count
+    (queries m0 .. m0 + count - 1)."""
+    row: np.ndarray
+    first_page: np.ndarray
+    end_page: np.ndarray
+    end_token: np.ndarray
+    m0: np.ndarray
+    count: np.ndarray
+
+    def __len__(self) -> int:
+        return int(self.row.size)
+
+    def segments(self, block_size: int) -> list:
+        return [Segment(int(a), int(b), int(e), list(range(int(m), int(m) + int(c))), int(r), block_size)
+                for r, a, b, e, m, c in zip(self.row, self.first_page, self.end_page, self.end_token, self.m0,
+                                            self.count)]
+
+
+@dataclass
 class TreePlan:
     items: np.ndarray          # int32 [n_shared + n_solo, ITEM_FIELDS]
     n_shared: int
@@ -51,15 +83,22 @@ class TreePlan:
     q_slot_offsets: np.ndarray  # int32 [N * Hkv + 1]
     q_slots: np.ndarray        # int32 [n_slots]
     n_slots: int
-    segments: list
+    seg: SegmentArrays
+    block_size: int
 
     @property
     def n_solo(self) -> int:
         return self.items.shape[0] - self.n_shared
 
+    @property
+    def segments(self) -> list:
+        return self.seg.segments(self.block_size)
+
     def unique_tokens(self) -> int:
         """Distinct cached token positions the batch reads (the same count in every layer)."""
-        return sum(s.tokens for s in self.segments)
+        if not len(self.seg):
+            return 0
+        return int((self.seg.end_token - self.seg.first_page * self.block_size).sum())
 
     def validate(self, Nq: int, Hkv: int, G: int, rows: int, table_stride: int, block_size: int) -> None:
         """Host check that every index the kernels take from the plan is in bounds."""
@@ -96,7 +135,8 @@ class TreePlan:
             raise ValueError("item partial slots out of range")
         if np.any((a[:, 7] < 0) | (a[:, 7].astype(np.int64) + a[:, 5] > mem.size)):
             raise ValueError("item member list out of range")
-        idx = np.concatenate([np.arange(o, o + n) for o, n in zip(a[:, 7], a[:, 5])])
+        tot = int(a[:, 5].sum())
+        idx = np.repeat(a[:, 7].astype(np.int64) - np.cumsum(a[:, 5]) + a[:, 5], a[:, 5]) + np.arange(tot)
         if np.any((mem[idx] < 0) | (mem[idx] >= Nq)):
             raise ValueError("member query index out of range")
 
@@ -114,90 +154,118 @@ class TreePlan:
         return cached[1]
 
 
-def find_segments(tables: list, lens: list, rows: list, block_size: int) -> list:
-    """Recursive partition of the batch's page paths (see module docstring)."""
+def table_array(tables) -> np.ndarray:
+    """Page tables (lists of block ids) as one int32 [N, P] array padded with -1."""
+    if isinstance(tables, np.ndarray):
+        return tables
+    P = max([len(t) for t in tables] + [1])
+    arr = np.full((len(tables), P), -1, dtype=np.int32)
+    for i, t in enumerate(tables):
+        arr[i, :len(t)] = t
+    return arr
+
+
+def common_prefix_pages(tab: np.ndarray, lens, block_size: int) -> np.ndarray:
+    """lcp[i]: leading pages on which rows i - 1 and i hold the same block id
+    with the same number of valid tokens (lcp[0] = 0). A shared partial page
+    ends the run."""
+    N, P = tab.shape
+    lcp = np.zeros(N, dtype=np.int64)
+    if N < 2:
+        return lcp
+    lens = np.asarray(lens, dtype=np.int64)
+    valid = np.clip(lens[:, None] - np.arange(P)[None, :] * block_size, 0, block_size)
+    ok = (tab[1:] == tab[:-1]) & (valid[1:] == valid[:-1]) & (valid[1:] > 0)
+    ok = np.concatenate([ok, np.zeros((N - 1, 1), dtype=bool)], axis=1)
+    lcp[1:] = np.argmin(ok, axis=1)
+    return lcp
+
+
+def segment_arrays(tables, lens, rows, block_size: int) -> SegmentArrays:
+    """Segments of the batch (see the module docstring)."""
+    tab = table_array(tables)
+    lens = np.asarray(lens, dtype=np.int64)
     B = block_size
-    npages = [(int(n) + B - 1) // B for n in lens]
-
-    def key(i, p):
-        return (int(tables[i][p]), min(B, int(lens[i]) - p * B))
-
-    segs: list[Segment] = []
-    stack = [(list(range(len(tables))), 0)]
-    while stack:
-        members, p = stack.pop()
-        members = [i for i in members if npages[i] > p]
-        if not members:
+    N = int(lens.size)
+    npg = ((lens + B - 1) // B).tolist()
+    lcp = common_prefix_pages(tab, lens, B).tolist()
+    out: list = []
+    for i in range(N):
+        lo, hi = lcp[i], npg[i]
+        if hi <= lo:
             continue
-        start = p
-        while True:
-            if any(npages[i] <= p for i in members):
-                break
-            k0 = key(members[0], p)
-            if any(key(i, p) != k0 for i in members[1:]):
-                break
-            p += 1
-            if k0[1] < B:
-                break
-        if p > start:
-            last_valid = key(members[0], p - 1)[1]
-            segs.append(Segment(start, p, (p - 1) * B + last_valid, list(members), int(rows[members[0]]), B))
-        rest = [i for i in members if npages[i] > p]
-        groups: dict = {}
-        for i in rest:
-            groups.setdefault(key(i, p), []).append(i)
-        for g in reversed(list(groups.values())):
-            stack.append((g, p))
-    return segs
+        j, r = i + 1, hi
+        while j < N and lcp[j] > lo:
+            if lcp[j] < r:
+                out.append((i, lcp[j], hi, j - i))  # pages [lcp[j], hi) of queries i .. j - 1
+                hi = r = lcp[j]
+            j += 1
+        out.append((i, lo, hi, j - i))
+    if not out:
+        z = np.zeros(0, dtype=np.int64)
+        return SegmentArrays(z, z, z, z, z, z)
+    a = np.array(out, dtype=np.int64)
+    owner = a[:, 0]
+    end_token = np.minimum(a[:, 2] * B, lens[owner])
+    return SegmentArrays(row=np.asarray(rows, dtype=np.int64)[owner], first_page=a[:, 1], end_page=a[:, 2],
+                         end_token=end_token, m0=owner, count=a[:, 3])
 
 
-def build_plan(tables: list, lens: list, rows: list, *, block_size: int, Hkv: int, G: int,
+def find_segments(tables, lens, rows, block_size: int) -> list:
+    """The batch's segments as Segment objects."""
+    return segment_arrays(tables, lens, rows, block_size).segments(block_size)
+
+
+def _items_of(sg: SegmentArrays, sel: np.ndarray, B: int, Hkv: int, chunk: int, cap: int):
+    """Items of the segments `sel`, chunk-major, then kv head, then member set."""
+    t0 = sg.first_page[sel] * B // 16
+    t1 = (sg.end_token[sel] + 15) // 16
+    cnt = sg.count[sel]
+    nch = (t1 - t0 + chunk - 1) // chunk
+    nset = (cnt + cap - 1) // cap
+    per = nch * Hkv * nset
+    tot = int(per.sum())
+    sid = np.repeat(np.arange(sel.size), per)
+    loc = np.arange(tot) - np.repeat(np.cumsum(per) - per, per)
+    ns = nset[sid]
+    iset = loc % ns
+    rest = loc // ns
+    h = rest % Hkv
+    ch = rest // Hkv
+    c0 = t0[sid] + ch * chunk
+    nt = np.minimum(chunk, t1[sid] - c0)
+    m_start = sg.m0[sel][sid] + iset * cap
+    m_cnt = np.minimum(cap, cnt[sid] - iset * cap)
+    return np.stack([sg.row[sel][sid], c0, nt, sg.end_token[sel][sid], h, m_cnt], axis=1), m_start
+
+
+def build_plan(tables, lens, rows, *, block_size: int, Hkv: int, G: int,
                chunk_tiles: int = 4, shared_chunk_tiles: int = 32, shared_min_groups: int = 3) -> TreePlan:
-    """Segments -> shared tasks, solo items and per-(query, head) partial slots."""
+    """Segments -> shared tasks, solo items and per-(query, head) partial slots.
+
+    ``tables``: the queries' page tables (lists, or an int32 [N, P] array whose
+    rows past a query's pages are ignored); ``rows``: each query's table row."""
     if G < 1 or 16 % G:
         raise ValueError("query heads per kv head must divide 16")
     if not 1 <= shared_chunk_tiles <= SHARED_MAX_TILES or chunk_tiles < 1:
         raise ValueError("chunk sizes must be >= 1 (shared: <= %d tiles)" % SHARED_MAX_TILES)
-    N = len(tables)
-    segs = find_segments(tables, lens, rows, block_size)
+    N = int(np.asarray(lens).size)
+    sg = segment_arrays(tables, lens, rows, block_size)
     mg = 16 // G
-    shared: list = []
-    solo: list = []
-    members: list = []
-    slots_of: list[list[int]] = [[] for _ in range(N * Hkv)]
-    n_slots = 0
-
-    def add(dst, seg, c0, nt, h, mem):
-        nonlocal n_slots
-        dst.append([seg.row, c0, nt, seg.end_token, h, len(mem), n_slots, len(members)])
-        members.extend(mem)
-        for m in mem:
-            slots_of[m * Hkv + h].append(n_slots)
-            n_slots += 1
-
-    for seg in segs:
-        t0 = seg.first_page * block_size // 16
-        t1 = (seg.end_token + 15) // 16
-        groups = (len(seg.members) + mg - 1) // mg
-        if groups >= shared_min_groups:
-            cap = WAVES_PER_WG * mg
-            sets = [seg.members[j:j + cap] for j in range(0, len(seg.members), cap)]
-            for c0 in range(t0, t1, shared_chunk_tiles):
-                nt = min(shared_chunk_tiles, t1 - c0)
-                for h in range(Hkv):
-                    for mem in sets:
-                        add(shared, seg, c0, nt, h, mem)
-        else:
-            sets = [seg.members[j:j + mg] for j in range(0, len(seg.members), mg)]
-            for c0 in range(t0, t1, chunk_tiles):
-                nt = min(chunk_tiles, t1 - c0)
-                for h in range(Hkv):
-                    for mem in sets:
-                        add(solo, seg, c0, nt, h, mem)
+    groups = (sg.count + mg - 1) // mg
+    shared = groups >= shared_min_groups
+    a_sh, m_sh = _items_of(sg, np.nonzero(shared)[0], block_size, Hkv, shared_chunk_tiles, WAVES_PER_WG * mg)
+    a_so, m_so = _items_of(sg, np.nonzero(~shared)[0], block_size, Hkv, chunk_tiles, mg)
+    body = np.concatenate([a_sh, a_so])
+    m_start = np.concatenate([m_sh, m_so])
+    m_cnt = body[:, 5]
+    first = np.cumsum(m_cnt) - m_cnt          # member offset = first slot of the item
+    items = np.concatenate([body, first[:, None], first[:, None]], axis=1).astype(np.int32)
+    n_slots = int(m_cnt.sum())
+    members = (np.repeat(m_start - first, m_cnt) + np.arange(n_slots)).astype(np.int32)
+    keys = members.astype(np.int64) * Hkv + np.repeat(body[:, 4], m_cnt)
     off = np.zeros(N * Hkv + 1, dtype=np.int32)
-    off[1:] = np.cumsum([len(s) for s in slots_of])
-    q_slots = np.array([s for lst in slots_of for s in lst] or [0], dtype=np.int32)
-    items = shared + solo
-    arr = np.array(items, dtype=np.int32).reshape(-1, ITEM_FIELDS) if items else np.zeros((0, ITEM_FIELDS), np.int32)
-    return TreePlan(items=arr, n_shared=len(shared), members=np.array(members, dtype=np.int32),
-                    q_slot_offsets=off, q_slots=q_slots, n_slots=n_slots, segments=segs)
+    off[1:] = np.cumsum(np.bincount(keys, minlength=N * Hkv))
+    q_slots = np.argsort(keys, kind="stable").astype(np.int32) if n_slots else np.zeros(1, np.int32)
+    return TreePlan(items=items.reshape(-1, ITEM_FIELDS), n_shared=int(a_sh.shape[0]), members=members,
+                    q_slot_offsets=off, q_slots=q_slots, n_slots=n_slots, seg=sg, block_size=block_size)

@@ -111,3 +111,79 @@ def test_tree_decode_rejects_bad_plans(gpu):
     plan.members[0] = len(tb.seq_ids)  # member index past the batch
     with pytest.raises(ValueError):
         ops.tree_decode(tb.q, tb.k_store, tb.v_store, block_tables=tb.block_tables, plan=plan)
+
+
+def test_tree_decode_counted_equals_tree_decode_and_replays_new_plans(gpu):
+    """mentat_tree_decode_counted (item counts in device memory, fixed grid of
+    workgroups striding over the items) gives tree_decode's output bit for bit
+    for the prefix-tree workload and a rollout-shaped batch (16 trees x 9
+    leaves under 256-token prompts) written one after the other into the same
+    fixed-capacity buffers; captured once in a graph, each replay after a new
+    plan is written (and uploaded outside the graph) gives that plan's eager
+    result, several times with eager work between the replays."""
+    print("case tree decode counted: cfg-3 trees and rollout-shaped trees, eager and captured", flush=True)
+    big = prefix_tree_batch(device="cuda", seed=0, max_blocks=8192)
+    small = prefix_tree_batch(n_trees=16, prefix=256, leaves=9, max_private=300, device="cuda", seed=4,
+                              max_blocks=8192)
+    Hkv, G = 8, 4
+    Nq = max(len(big.seq_ids), len(small.seq_ids))
+    plans, wants = [], []
+    for tb in (big, small):
+        plan = build_plan(tb.tables, tb.lens, tb.rows, block_size=16, Hkv=Hkv, G=G)
+        plan.validate(len(tb.seq_ids), Hkv, G, tb.block_tables.shape[0], tb.block_tables.shape[1], 16)
+        plans.append(plan)
+        wants.append(ops.tree_decode(tb.q, tb.k_store, tb.v_store, block_tables=tb.block_tables, plan=plan,
+                                     scale=tb.scale))
+    bufs = ops.TreePlanBuffers(torch.device("cuda"), Nq, Hkv, max_shared=max(p.n_shared for p in plans) + 5,
+                               max_solo=max(p.n_solo for p in plans) + 100,
+                               max_slots=max(p.n_slots for p in plans) + 64)
+    q = torch.zeros(Nq, 32, 128, dtype=torch.bfloat16, device="cuda")
+    out = torch.zeros_like(q)
+
+    def load(i):
+        tb = (big, small)[i]
+        q.zero_()
+        q[:len(tb.seq_ids)] = tb.q
+        bufs.write(plans[i], len(tb.seq_ids))
+        bufs.upload()
+        return tb
+
+    # the two batches live in different managers: one call per manager's stores
+    for i in (0, 1, 0):
+        tb = load(i)
+        ops.tree_decode_counted(q, tb.k_store, tb.v_store, block_tables=tb.block_tables, bufs=bufs, scale=tb.scale,
+                                out=out)
+        torch.cuda.synchronize()
+        n = len(tb.seq_ids)
+        assert torch.equal(out[:n], wants[i]), i
+        assert torch.equal(out[n:], torch.zeros_like(out[n:]))
+    # captured: the small batch's stores, plans of that batch with the tables trimmed to fewer queries
+    tb = load(1)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        ops.tree_decode_counted(q, tb.k_store, tb.v_store, block_tables=tb.block_tables, bufs=bufs, scale=tb.scale,
+                                out=out)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=side):
+        ops.tree_decode_counted(q, tb.k_store, tb.v_store, block_tables=tb.block_tables, bufs=bufs, scale=tb.scale,
+                                out=out)
+    torch.cuda.synchronize()
+    for n_keep in (len(tb.seq_ids), 60, 17, len(tb.seq_ids)):
+        plan = build_plan([tb.tables[i] for i in range(n_keep)], tb.lens[:n_keep], tb.rows[:n_keep], block_size=16,
+                          Hkv=Hkv, G=G)
+        plan.validate(n_keep, Hkv, G, tb.block_tables.shape[0], tb.block_tables.shape[1], 16)
+        want = ops.tree_decode(tb.q[:n_keep].contiguous(), tb.k_store, tb.v_store, block_tables=tb.block_tables,
+                               plan=plan, scale=tb.scale)
+        torch.cuda.synchronize()
+        q.zero_()
+        q[:n_keep] = tb.q[:n_keep]
+        bufs.write(plan, n_keep)
+        bufs.upload()
+        out.fill_(7.0)
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out[:n_keep], want), n_keep
+        assert torch.equal(out[n_keep:Nq], torch.zeros_like(out[n_keep:Nq])), n_keep
