@@ -566,6 +566,11 @@ def run_e2e(args, dev) -> dict:
         "results": sum(len(r) for r in results), "kv_blocks_peak": d["kv_blocks_peak"],
         "weight_bytes": wbytes,
     }
+    graphs = gen.wrapper.graphs
+    if graphs is not None:
+        config["attention"] = ("prefix-tree decode from layer %d (plans sharing pages: %d steps, without: %d)"
+                               % (graphs._tree_from(), graphs.tree_steps, graphs.tree_fallbacks)
+                               if graphs.tree else "paged decode")
     cpu = None
     if not args.no_cpu_baseline:
         cpu = _cpu_baseline_e2e(model, prompts[0], new_tokens, knobs, args.cpu_seconds)

@@ -184,6 +184,22 @@ int mentat_tree_decode_counted(const void* q, const void* k_store, const void* v
                                int max_slots, void* out, int Nq, int Hq, int Hkv, int D, int block_size,
                                float scale, int dtype, void* workspace, size_t workspace_bytes, void* stream);
 
+/* Host planner of the prefix-tree decode (no device work): the plan of
+ * mentat_amd/tree_plan.py:build_plan for N queries, written into the arrays
+ * mentat_tree_decode_counted reads. Segments are the pages a run of
+ * neighbouring queries holds through the same block ids (forks copy their
+ * parent's ids, core/paged_kv_cache.py:152-170); share = 0 gives every query
+ * one segment of its own. tables: host block ids, query i's at
+ * tables[qrows[i] * table_stride ...]; lens: tokens per query.
+ * Outputs: counts [3] = n_shared, n_solo, n_slots; items [(max_shared +
+ * max_solo) * 8] with the solo items right after the shared ones; members and
+ * q_slots [max_slots]; q_slot_offsets [N * Hkv + 1]. Returns MENTAT_ESPACE
+ * when a capacity is exceeded (the outputs are then incomplete). */
+int mentat_tree_plan(const int32_t* tables, int64_t table_stride, const int32_t* qrows, const int32_t* lens, int N,
+                     int block_size, int Hkv, int G, int chunk_tiles, int shared_chunk_tiles, int shared_min_groups,
+                     int share, int32_t* counts, int32_t* items, int max_shared, int max_solo, int32_t* members,
+                     int32_t* q_slot_offsets, int32_t* q_slots, int max_slots);
+
 /* ------------------------------------------------------------------------
  * Prefill attention: causal (optionally sliding-window) attention over one
  * batch of prompts, GQA.

@@ -86,6 +86,15 @@ SIGNATURES: dict[str, tuple] = {
             _c_void_p, _c_size, _c_void_p,  # workspace, workspace_bytes, stream
         ],
     ),
+    "mentat_tree_plan": (
+        _c_int,
+        [
+            _c_void_p, _c_i64, _c_void_p, _c_void_p, _c_int,  # tables, table_stride, qrows, lens, N
+            _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,  # block_size, Hkv, G, chunks, min groups, share
+            _c_void_p, _c_void_p, _c_int, _c_int, _c_void_p,  # counts, items, max_shared, max_solo, members
+            _c_void_p, _c_void_p, _c_int,  # q_slot_offsets, q_slots, max_slots
+        ],
+    ),
     "mentat_prefill_attention": (
         _c_int,
         [

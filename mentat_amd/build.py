@@ -1,4 +1,5 @@
-"""Build libmentat_hip.so (gfx950) from mentat_amd/csrc/*.hip with hipcc.
+"""Build libmentat_hip.so (gfx950) from mentat_amd/csrc/*.hip with hipcc (and
+the host-only mentat_amd/csrc/*.cpp with the host compiler).
 
 Every call recompiles all sources (objects go to mentat_amd/_build/, the
 library to mentat_amd/lib/libmentat_hip.so). Usage: ``python -m mentat_amd.build``.
@@ -51,15 +52,29 @@ def _compile(src: str) -> str:
     return obj
 
 
+# Host-only sources (planners run on the CPU each step) go through the host compiler.
+CXX = shutil.which("g++") or "g++"
+HOST_FLAGS = ["-O3", "-std=c++17", "-fPIC", "-Wall", "-Wno-unused-function"]
+
+
+def _compile_host(src: str) -> str:
+    obj = os.path.join(BUILD, os.path.basename(src).replace(".cpp", "_host.o"))
+    _run([CXX, *HOST_FLAGS, "-I", os.path.join(os.path.dirname(HERE), "include"), "-c", src, "-o", obj])
+    return obj
+
+
 def build(verbose: bool = True) -> str:
     os.makedirs(BUILD, exist_ok=True)
     os.makedirs(LIBDIR, exist_ok=True)
     srcs = sorted(glob.glob(os.path.join(CSRC, "*.hip")))
+    host = sorted(glob.glob(os.path.join(CSRC, "*.cpp")))
     if not srcs:
         raise RuntimeError(f"no HIP sources under {CSRC}")
-    workers = max(1, min(len(srcs), os.cpu_count() or 1, 16))
+    workers = max(1, min(len(srcs) + len(host), os.cpu_count() or 1, 16))
     with cf.ThreadPoolExecutor(workers) as ex:
-        objs = list(ex.map(_compile, srcs))
+        jobs = [ex.submit(_compile, s) for s in srcs] + [ex.submit(_compile_host, s) for s in host]
+        objs = [j.result() for j in jobs]
+    srcs = srcs + host
     tmp = LIB + ".tmp"
     _run([HIPCC, "-shared", f"--offload-arch={ARCH}", "-fPIC", *objs, "-o", tmp])
     os.replace(tmp, LIB)

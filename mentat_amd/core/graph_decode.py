@@ -59,7 +59,7 @@ import numpy as np
 import torch
 
 from .. import ops
-from .._lib import get_lib
+from .._lib import LAYOUT_NATIVE, get_lib
 from ..adapters.model_adapter import _HFDecoderAdapter
 
 __all__ = ["DecodeGraphs", "BUCKETS"]
@@ -137,10 +137,30 @@ def _merge_linears(lins) -> torch.Tensor:
 # step at 144 leaves against 9.07 for two and three).
 SPLIT_LAYERS = 2
 
+# Attention of the layers after the first graph runs the prefix-tree decode
+# (mentat_tree_decode_counted): pages that forked leaves share are read once
+# per group of leaves. Its plan is made while the first graph runs, by the
+# native planner from the host copy of layer 0's tables (the sharing pattern
+# is every layer's), and copied in before the second graph.
+TREE_DECODE = True
+
+
+def _tree_caps(nb: int, Hkv: int, max_len: int) -> tuple:
+    """(max_shared, max_solo, max_slots) of a bucket's plan buffers. A plan
+    without sharing (each query one segment, solo items of 4 tiles) needs at
+    most nb * ceil(tiles / 4) * Hkv items and slots; a query cut into k
+    segments adds at most k - 1 chunks, and k <= 9 is allowed before the
+    planner falls back to that plan. Shared tasks (segments of >= 9 queries)
+    need one item per 32 tiles per head per 32 queries."""
+    tiles = -(-max_len // 16)
+    solo = nb * (-(-tiles // 4) + 8) * Hkv
+    shared = max(1, -(-nb // 9)) * (-(-tiles // 32) + 2) * Hkv * 2
+    return shared, solo, solo
+
 
 class _Bucket:
     __slots__ = ("n", "graph", "graph2", "state", "dev", "host", "host_np", "logits", "hidden", "version",
-                 "copied")
+                 "copied", "tree", "tree_read")
 
 
 class DecodeGraphs:
@@ -152,6 +172,7 @@ class DecodeGraphs:
         self.dev = wrapper.device
         self._graphs: dict[int, _Bucket] = {}
         self._stream = torch.cuda.Stream(self.dev)
+        self._copy_stream = torch.cuda.Stream(self.dev)  # tree plan copies, overlapping the first graph
         self._ws = None
         self.captures = 0
         self.fused = _fusable(self.a, self.m.dtype)
@@ -160,6 +181,11 @@ class DecodeGraphs:
         self._w_gu: list = []
         if self.merged:
             self._merge()
+        Hq, Hkv = self.a.num_attention_heads, self.a.num_key_value_heads
+        self.G = Hq // Hkv if Hq % Hkv == 0 else 0
+        self.tree = bool(TREE_DECODE and self.m.layout == LAYOUT_NATIVE and self.G and 16 % self.G == 0)
+        self.tree_steps = 0       # steps whose plan shared pages
+        self.tree_fallbacks = 0   # steps planned without sharing (a capacity was exceeded)
         if buckets is None:
             buckets = MERGED_BUCKETS if self.merged else BUCKETS
         self.buckets = tuple(sorted(buckets))
@@ -214,13 +240,27 @@ class DecodeGraphs:
         plans[:, :, n:] = -1               # dst block -1: skipped by the append kernel
         plans[:, 6, n:] = 0
 
-    def _forward(self, buf: torch.Tensor, nb: int, lo: int = 0, hi=None, state=None):
+    def _attention(self, q: torch.Tensor, layer_idx: int, rows: torch.Tensor, max_seqlen: int, tree):
+        """One layer's decode attention of the step: the prefix-tree decode from
+        the layer the tree plan is ready for, the paged decode before it."""
+        m = self.m
+        if tree is not None and layer_idx >= self._tree_from():
+            return ops.tree_decode_counted(q, m._k_store, m._v_store, block_tables=m._tables[layer_idx], bufs=tree)
+        return ops.paged_decode(q, m._k_store, m._v_store, layout=m.layout, block_tables=m._tables[layer_idx],
+                                seq_lens=m._lens[layer_idx], seq_rows=rows, max_seqlen=max_seqlen)
+
+    def _tree_from(self) -> int:
+        """First layer on the tree decode: the second graph's (its plan is made
+        while the first runs), or layer 0 with one graph per step."""
+        return self._split_layers()
+
+    def _forward(self, buf: torch.Tensor, nb: int, lo: int = 0, hi=None, state=None, tree=None):
         """Layers lo .. hi - 1 of the step (all by default). The first range
         starts from the embeddings; a range that ends before the last layer
         returns the state the next range starts from, the last one returns
         (logits, final hidden)."""
         if self.fused:
-            return self._forward_fused(buf, nb, lo, hi, state)
+            return self._forward_fused(buf, nb, lo, hi, state, tree)
         a, m = self.a, self.m
         L = m.num_layers
         hi = L if hi is None else hi
@@ -241,9 +281,7 @@ class DecodeGraphs:
             ops.kv_append(k.squeeze(1).to(m.dtype).contiguous(), v.squeeze(1).to(m.dtype).contiguous(),
                           m._k_store, m._v_store, plans[layer_idx], block_size=m.block_size, layout=m.layout,
                           block_tables=m._tables[layer_idx], seq_lens=m._lens[layer_idx])
-            o = ops.paged_decode(q.squeeze(1).contiguous(), m._k_store, m._v_store, layout=m.layout,
-                                 block_tables=m._tables[layer_idx], seq_lens=m._lens[layer_idx], seq_rows=rows,
-                                 max_seqlen=max_seqlen)
+            o = self._attention(q.squeeze(1).contiguous(), layer_idx, rows, max_seqlen, tree)
             attn_out = attn.o_proj(o.reshape(1, nb, -1))
             hidden = a.apply_post_attn_residual(block, residual, attn_out)
             residual = hidden
@@ -254,7 +292,7 @@ class DecodeGraphs:
         hidden = a.final_norm(hidden).squeeze(0)
         return a.lm_head(hidden), hidden
 
-    def _forward_fused(self, buf: torch.Tensor, nb: int, lo: int = 0, hi=None, state=None):
+    def _forward_fused(self, buf: torch.Tensor, nb: int, lo: int = 0, hi=None, state=None, tree=None):
         """_forward with the layer glue fused (see the module docstring); the
         state between layer ranges is (normalised input, residual stream)."""
         a, m = self.a, self.m
@@ -289,9 +327,7 @@ class DecodeGraphs:
             ops.kv_append(k.to(m.dtype).contiguous(), v.to(m.dtype).contiguous(),
                           m._k_store, m._v_store, plans[layer_idx], block_size=m.block_size, layout=m.layout,
                           block_tables=m._tables[layer_idx], seq_lens=m._lens[layer_idx])
-            o = ops.paged_decode(q, m._k_store, m._v_store, layout=m.layout,
-                                 block_tables=m._tables[layer_idx], seq_lens=m._lens[layer_idx], seq_rows=rows,
-                                 max_seqlen=max_seqlen)
+            o = self._attention(q.contiguous(), layer_idx, rows, max_seqlen, tree)
             attn_out = attn.o_proj(o.reshape(1, nb, -1))
             ln = block.post_attention_layernorm
             x, hidden = ops.rmsnorm(attn_out, ln.weight, ln.variance_epsilon, residual=hidden)
@@ -309,13 +345,19 @@ class DecodeGraphs:
         return a.lm_head(x), x
 
     def _workspace(self) -> None:
-        """Size the capture stream's decode workspace for the largest bucket."""
-        if self._ws is not None:
-            return
+        """Size the capture stream's decode workspace for the largest bucket
+        (paged decode, and the tree decode's partial slots). It only grows when
+        the tables have grown, and then every graph is captured again."""
         a, m = self.a, self.m
-        nbytes = get_lib().mentat_paged_decode_workspace_bytes(
-            m.layout, self.max_batch, a.num_attention_heads, a.num_key_value_heads, a.head_dim, m.block_size,
-            m._pages_cap * m.block_size, 0, 0)
+        lib = get_lib()
+        Hq, Hkv, D = a.num_attention_heads, a.num_key_value_heads, a.head_dim
+        nbytes = lib.mentat_paged_decode_workspace_bytes(m.layout, self.max_batch, Hq, Hkv, D, m.block_size,
+                                                         m._pages_cap * m.block_size, 0, 0)
+        if self.tree:
+            slots = _tree_caps(self.max_batch, Hkv, m._pages_cap * m.block_size)[2]
+            nbytes = max(nbytes, lib.mentat_tree_decode_workspace_bytes(slots, Hq, Hkv, D))
+        if self._ws is not None and self._ws.numel() >= nbytes:
+            return
         with torch.cuda.stream(self._stream):
             self._ws = ops.workspace(self.dev, nbytes)
 
@@ -334,6 +376,14 @@ class DecodeGraphs:
         self._fill_padding(b.host_np, nb, 0)
         b.dev = torch.empty(size, dtype=torch.int32, device=self.dev)
         b.dev.copy_(b.host)
+        b.tree = None
+        if self.tree:  # zero-filled: no items, every query's output zero, until a plan is written
+            caps = _tree_caps(nb, self.a.num_key_value_heads, m._pages_cap * m.block_size)
+            b.tree = ops.TreePlanBuffers(self.dev, nb, self.a.num_key_value_heads, *caps)
+            # recorded after each replay of the graph that reads the plan: the
+            # next plan's copy waits for it
+            b.tree_read = torch.cuda.Event()
+            b.tree_read.record(torch.cuda.current_stream(self.dev))
         # Recorded after each step's last copy out of b.host: the next step waits
         # for it before it rewrites the pinned staging.
         b.copied = torch.cuda.Event()
@@ -342,7 +392,7 @@ class DecodeGraphs:
         s.wait_stream(torch.cuda.current_stream(self.dev))
         with torch.cuda.stream(s):
             for _ in range(2):  # warm-up (library handles, GEMM selection) on all-padding input
-                self._forward(b.dev, nb)
+                self._forward(b.dev, nb, tree=b.tree)
         torch.cuda.current_stream(self.dev).wait_stream(s)
         g = torch.cuda.CUDAGraph()
         g2 = None
@@ -353,14 +403,14 @@ class DecodeGraphs:
         try:
             if k:
                 with torch.cuda.graph(g, stream=s):
-                    b.state = self._forward(b.dev, nb, 0, k)
+                    b.state = self._forward(b.dev, nb, 0, k, tree=b.tree)
                 g2 = torch.cuda.CUDAGraph()
                 with torch.cuda.graph(g2, pool=g.pool(), stream=s):
-                    b.logits, b.hidden = self._forward(b.dev, nb, k, None, b.state)
+                    b.logits, b.hidden = self._forward(b.dev, nb, k, None, b.state, tree=b.tree)
             else:
                 b.state = None
                 with torch.cuda.graph(g, stream=s):
-                    b.logits, b.hidden = self._forward(b.dev, nb)
+                    b.logits, b.hidden = self._forward(b.dev, nb, tree=b.tree)
         finally:
             if gc_on:
                 gc.enable()
@@ -411,6 +461,9 @@ class DecodeGraphs:
             plans_h[:k, :, :n] = plan[:k]
             b.dev[:cut].copy_(b.host[:cut], non_blocking=True)
             b.graph.replay()
+            # while the first graph runs: the tree plan (layer 0's tables are
+            # final), then the later layers' appends
+            self._plan_tree(b, seq_ids, rows)
             plan = m.plan_append_step_finish(st)
             if int(plan[k:, 4].max()) >= m._pages_cap:
                 raise RuntimeError("DecodeGraphs: a later layer's append needs more table pages than the first")
@@ -418,14 +471,46 @@ class DecodeGraphs:
             b.dev[cut:].copy_(b.host[cut:], non_blocking=True)
             b.copied.record()
             b.graph2.replay()
+            if b.tree is not None:
+                b.tree_read.record()
         else:
             plans_h[:, :, :n] = plan
             b.dev.copy_(b.host, non_blocking=True)
+            self._plan_tree(b, seq_ids, rows)
             b.copied.record()
             b.graph.replay()
             if b.graph2 is not None:
                 b.graph2.replay()
+            if b.tree is not None:
+                b.tree_read.record()
         return b.logits[:n].clone(), b.hidden[:n].clone()
+
+    def _plan_tree(self, b: _Bucket, seq_ids: list, rows: list) -> None:
+        """The step's prefix-tree plan (after layer 0's appends are planned:
+        the tables and lengths attention reads) into the bucket's buffers, and
+        their copy to the device queued."""
+        if b.tree is None:
+            return
+        m = self.m
+        seqs = m._sequences
+        n = len(seq_ids)
+        lens = np.fromiter((seqs[s].num_tokens[0] for s in seq_ids), dtype=np.int32, count=n)
+        _, _, _, shared = b.tree.plan(m.host_tables0(), np.asarray(rows, dtype=np.int32), lens, m.block_size,
+                                      self.G)
+        if shared:
+            self.tree_steps += 1
+        else:
+            self.tree_fallbacks += 1
+        # The copies run on a side stream beside the first graph, once the
+        # previous replay has read the device plan; the step's stream waits for
+        # them before its next work (the later layers' copy and the second
+        # graph), so the staging event recorded after that covers them too.
+        main = torch.cuda.current_stream(self.dev)
+        cs = self._copy_stream
+        cs.wait_event(b.tree_read)
+        with torch.cuda.stream(cs):
+            b.tree.upload()
+        main.wait_stream(cs)
 
     def _split_layers(self) -> int:
         """Layers of the first graph (0: one graph for the whole step)."""

@@ -196,6 +196,10 @@ class PagedKVCacheManager:
         self._tables = torch.zeros(L, self._rows_cap, self._pages_cap, dtype=torch.int32, device=self.device)
         self._lens = torch.zeros(L, self._rows_cap, dtype=torch.int32, device=self.device)
         self._free_rows: list[int] = list(range(self._rows_cap - 1, -1, -1))
+        # Host copy of layer 0's table rows (indexed like the device rows): the
+        # prefix-tree planner compares block ids on it each decode step. Every
+        # layer shares layer 0's sharing pattern, so one layer is enough.
+        self._host_t0 = np.zeros((self._rows_cap, self._pages_cap), dtype=np.int32)
         self._rows_cache: dict[tuple, torch.Tensor] = {}
         self._cu_cache: dict[tuple, torch.Tensor] = {}
         # Bumped whenever _tables / _lens are reallocated: captured launches that
@@ -217,6 +221,9 @@ class PagedKVCacheManager:
         n = torch.zeros(self.num_layers, new, dtype=torch.int32, device=self.device)
         n[:, :old] = self._lens
         self._tables, self._lens, self._rows_cap = t, n, new
+        h = np.zeros((new, self._host_t0.shape[1]), dtype=np.int32)
+        h[:old] = self._host_t0
+        self._host_t0 = h
         self._free_rows = list(range(new - 1, old - 1, -1)) + self._free_rows
         self.tables_version += 1
 
@@ -229,8 +236,29 @@ class PagedKVCacheManager:
         t = torch.zeros(self.num_layers, self._rows_cap, new, dtype=torch.int32, device=self.device)
         t[:, :, : self._pages_cap] = self._tables
         self._tables, self._pages_cap = t, new
+        self._widen_host_t0(new)
         self._rows_cache.clear()
         self.tables_version += 1
+
+    def _widen_host_t0(self, pages: int) -> None:
+        w = self._host_t0.shape[1]
+        if pages <= w:
+            return
+        while w < pages:
+            w *= 2
+        h = np.zeros((self._host_t0.shape[0], w), dtype=np.int32)
+        h[:, : self._host_t0.shape[1]] = self._host_t0
+        self._host_t0 = h
+
+    def _host_t0_row(self, seq: SequenceState) -> None:
+        t = seq.page_table[0]
+        self._widen_host_t0(len(t))
+        self._host_t0[seq.row, : len(t)] = t
+
+    def host_tables0(self) -> np.ndarray:
+        """Layer 0's block ids on the host, [rows, stride] int32 indexed by table
+        row (entries past a row's pages are stale)."""
+        return self._host_t0
 
     def reserve(self, rows: int, pages: int) -> None:
         """Grow the device tables to at least ``rows`` free rows and ``pages``
@@ -284,6 +312,8 @@ class PagedKVCacheManager:
             row=self._take_row(),
         )
         self._sequences[child_id] = child
+        n0 = len(tables[0]) if tables else 0
+        self._host_t0[child.row, :n0] = self._host_t0[parent.row, :n0]
         if self.device.type == "cuda":
             n_entries = max((len(t) for t in tables), default=0)
             idx = torch.tensor([parent.row, child.row], dtype=torch.int32).to(self.device, non_blocking=True)
@@ -336,6 +366,8 @@ class PagedKVCacheManager:
         seq.num_tokens[layer_idx] += num_new
         if num_new:
             plan[5, num_new - 1] = seq.num_tokens[layer_idx]
+        if layer_idx == 0:
+            self._host_t0_row(seq)
         return plan
 
     def plan_append_batched(self, seq_ids: list[int], layer_idx: int) -> np.ndarray:
@@ -371,8 +403,12 @@ class PagedKVCacheManager:
             rows.append(seq.row)
             pages.append(len(table) - 1)
             lens.append(nt[L])
-        return np.array([dst, slots, cows, rows, pages, lens, list(range(len(seq_ids)))],
+        plan = np.array([dst, slots, cows, rows, pages, lens, list(range(len(seq_ids)))],
                         dtype=np.int32).reshape(7, len(seq_ids))
+        if L == 0 and seq_ids:
+            self._widen_host_t0(int(plan[4].max()) + 1)
+            self._host_t0[plan[3], plan[4]] = plan[0]
+        return plan
 
     def plan_append_step(self, seq_ids: list[int]) -> np.ndarray:
         """Host half of one decode step's appends for every layer: the int32
@@ -624,6 +660,7 @@ class PagedKVCacheManager:
 
     def _upload_row(self, seq: SequenceState) -> None:
         """Re-write a sequence's device table row and lengths from the host lists."""
+        self._host_t0_row(seq)
         if self.device.type != "cuda":
             return
         npg = max((len(t) for t in seq.page_table), default=0)

@@ -17,6 +17,7 @@ from ._lib import (
     DTYPE_CODES,
     LAYOUT_NATIVE,
     LAYOUT_REFERENCE,
+    MENTAT_ESPACE,
     MentatError,
     check,
     get_lib,
@@ -576,25 +577,27 @@ def philox4x32_10(counters: torch.Tensor, keys: torch.Tensor) -> torch.Tensor:
 class TreePlanBuffers:
     """Device arrays of prefix-tree plans with fixed capacities, refilled per
     call (for launches captured once and replayed with new plans): one int32
-    buffer holding counts [2], items [max_items, 8], members [max_slots],
-    q_slot_offsets [Nq * Hkv + 1], q_slots [max_slots], and a pinned host twin
-    the plan is written into before one copy."""
+    buffer holding counts [2], q_slot_offsets [Nq * Hkv + 1], items
+    [max_items, 8], members [max_slots] and q_slots [max_slots], and a pinned
+    host twin the plan is written into; upload copies the parts in use."""
 
     def __init__(self, device, Nq: int, Hkv: int, max_shared: int, max_solo: int, max_slots: int):
         self.Nq, self.Hkv = Nq, Hkv
         self.max_shared, self.max_solo, self.max_slots = max_shared, max_solo, max_slots
         mi = max_shared + max_solo
-        self._cuts = np.cumsum([0, 2, 8 * max(mi, 1), max(max_slots, 1), Nq * Hkv + 1, max(max_slots, 1)])
+        # regions: counts | q_slot_offsets | items | members | q_slots
+        self._cuts = np.cumsum([0, 2, Nq * Hkv + 1, 8 * max(mi, 1), max(max_slots, 1), max(max_slots, 1)])
         n = int(self._cuts[-1])
         self.host = torch.zeros(n, dtype=torch.int32, pin_memory=True)
         self.host_np = self.host.numpy()
         self.dev = torch.zeros(n, dtype=torch.int32, device=device)
         c = self._cuts
         self.counts = self.dev[c[0]:c[1]]
-        self.items = self.dev[c[1]:c[2]]
-        self.members = self.dev[c[2]:c[3]]
-        self.q_slot_offsets = self.dev[c[3]:c[4]]
+        self.q_slot_offsets = self.dev[c[1]:c[2]]
+        self.items = self.dev[c[2]:c[3]]
+        self.members = self.dev[c[3]:c[4]]
         self.q_slots = self.dev[c[4]:c[5]]
+        self._used = (mi, max_slots)  # items and slots the last plan holds
 
     def fits(self, plan) -> bool:
         return plan.n_shared <= self.max_shared and plan.n_solo <= self.max_solo and plan.n_slots <= self.max_slots
@@ -604,16 +607,55 @@ class TreePlanBuffers:
         _require(self.fits(plan), "the plan exceeds the buffers' capacities")
         c, h = self._cuts, self.host_np
         h[0], h[1] = plan.n_shared, plan.n_solo
-        k = plan.items.size
-        h[c[1]:c[1] + k] = plan.items.reshape(-1)
-        h[c[2]:c[2] + plan.members.size] = plan.members
-        off = h[c[3]:c[4]]
+        off = h[c[1]:c[2]]
         off[:n * self.Hkv + 1] = plan.q_slot_offsets
         off[n * self.Hkv + 1:] = plan.q_slot_offsets[-1]
-        h[c[4]:c[4] + plan.q_slots.size] = plan.q_slots
+        k = plan.items.size
+        h[c[2]:c[2] + k] = plan.items.reshape(-1)
+        h[c[3]:c[3] + plan.n_slots] = plan.members[:plan.n_slots]
+        h[c[4]:c[4] + plan.n_slots] = plan.q_slots[:plan.n_slots]
+        self._used = (plan.items.shape[0], plan.n_slots)
 
     def upload(self) -> None:
-        self.dev.copy_(self.host, non_blocking=True)
+        """Queue the copies of the parts the last plan uses (three copies)."""
+        c = self._cuts
+        items, slots = self._used
+        a = int(c[2]) + 8 * items
+        self.dev[:a].copy_(self.host[:a], non_blocking=True)
+        if slots:
+            for lo in (int(c[3]), int(c[4])):
+                self.dev[lo:lo + slots].copy_(self.host[lo:lo + slots], non_blocking=True)
+
+    def plan(self, tables: np.ndarray, qrows: np.ndarray, lens: np.ndarray, block_size: int, G: int,
+             chunk_tiles: int = 4, shared_chunk_tiles: int = 32, shared_min_groups: int = 3) -> tuple:
+        """Plan n queries with the native planner (mentat_tree_plan) straight
+        into the host twin. tables: host int32 [rows, stride] block ids indexed
+        by table row; qrows, lens: int32 per query. When a capacity is exceeded
+        the queries get a plan without sharing (one segment each), which the
+        capacities hold by construction. Returns (n_shared, n_solo, n_slots, shared)."""
+        n = int(qrows.size)
+        _require(n <= self.Nq, "more queries than the buffers hold")
+        _require(tables.dtype == np.int32 and tables.flags.c_contiguous, "tables must be C-contiguous int32")
+        qrows = np.ascontiguousarray(qrows, dtype=np.int32)
+        lens = np.ascontiguousarray(lens, dtype=np.int32)
+        c, h = self._cuts, self.host_np
+        base = h.ctypes.data
+        cnt = np.zeros(3, dtype=np.int32)
+        off = h[c[1]:c[2]]
+        lib = get_lib()
+        for share in (1, 0):
+            st = lib.mentat_tree_plan(
+                tables.ctypes.data, tables.shape[1], qrows.ctypes.data, lens.ctypes.data, n, block_size,
+                self.Hkv, G, chunk_tiles, shared_chunk_tiles, shared_min_groups, share, cnt.ctypes.data,
+                base + 4 * int(c[2]), self.max_shared, self.max_solo, base + 4 * int(c[3]),
+                base + 4 * int(c[1]), base + 4 * int(c[4]), self.max_slots)
+            if st == 0:
+                break
+            _require(st == MENTAT_ESPACE and share, f"mentat_tree_plan failed ({st})")
+        h[0], h[1] = cnt[0], cnt[1]
+        off[n * self.Hkv + 1:] = off[n * self.Hkv]
+        self._used = (int(cnt[0] + cnt[1]), int(cnt[2]))
+        return int(cnt[0]), int(cnt[1]), int(cnt[2]), bool(share)
 
 
 def tree_decode_counted(

@@ -117,6 +117,9 @@ def test_captured_steps_match_eager_steps(gpu, monkeypatch, split):
     assert len(used) >= 3, sizes                     # several buckets were replayed in turn
     assert g.captures == len(used), (g.captures, used)  # each captured once, then replayed
     assert all((b.graph2 is not None) == (split < 2) for b in g._graphs.values())
+    # the captured layers after the first graph (all of them with one graph) ran
+    # the prefix-tree decode on plans that shared the forked pages
+    assert g.tree and g.tree_steps == len(sizes) and g.tree_fallbacks == 0
 
 
 @pytest.mark.parametrize("split", [1, 2])

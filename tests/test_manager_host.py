@@ -19,10 +19,13 @@ def _same_state(m: PagedKVCacheManager, c: OracleCache):
     assert m.allocator._free == c.alloc.free
     assert m.allocator.peak_used == c.alloc.peak
     assert set(m._sequences) == set(c.tables)
+    h0 = m.host_tables0()
     for sid, st in m._sequences.items():
         assert st.page_table == c.tables[sid]
         assert st.num_tokens == c.ntok[sid]
         assert st.tokens_in_last_block == c.tilb[sid]
+        # the host copy of layer 0's rows that the tree planner reads
+        assert h0[st.row, :len(st.page_table[0])].tolist() == st.page_table[0]
 
 
 @pytest.mark.parametrize("seed", range(5))
