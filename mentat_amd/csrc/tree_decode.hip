@@ -315,7 +315,10 @@ __device__ __forceinline__ void tree_shared(const TreeParams& p, const int32_t* 
   // Steps of two tiles; tiles 2s, 2s+1 go to LDS stage s & 1. kTreePrefetch
   // tiles are in flight ahead of the one being written (ring of kTreePrefetch
   // + 2 registers, so a step's loads never overwrite what it writes). The
-  // loop is fully unrolled: with no back edge every wait counts exactly.
+  // steps are unrolled and nested (step s + 1 sits inside step s's branch):
+  // with no back edge and no join between steps, the wait before a tile's LDS
+  // write counts exactly the loads issued after it. (Sibling branches would
+  // join the path that skipped step s - 1, and the waits would assume it.)
   constexpr int R = kTreePrefetch + 2;
   uint4 pf[R];
   static_for<kTreePrefetch>([&](auto ic) __attribute__((always_inline)) {
@@ -331,10 +334,10 @@ __device__ __forceinline__ void tree_shared(const TreeParams& p, const int32_t* 
     const int qidx = (active && g0 + cm < nmem) ? p.members[moff + g0 + cm] : -1;
     w.init(p, lane, qidx, head, G);
   }
-  static_for<kTreeSharedMaxTiles / 2>([&](auto sc_) __attribute__((always_inline)) {
+  auto step = [&](auto self, auto sc_) __attribute__((always_inline)) -> void {
     constexpr int st = decltype(sc_)::value;
     constexpr int i0 = 2 * st;
-    if (i0 < ntile) {
+    {  // i0 < ntile holds here: step 0 runs for ntile >= 1, step s + 1 for 2s + 2 < ntile
       if constexpr (i0 + kTreePrefetch < kTreeSharedMaxTiles)
         pf[(i0 + kTreePrefetch) % R] = issue(std::integral_constant<int, i0 + kTreePrefetch>{});
       if constexpr (i0 + 1 + kTreePrefetch < kTreeSharedMaxTiles)
@@ -371,7 +374,11 @@ __device__ __forceinline__ void tree_shared(const TreeParams& p, const int32_t* 
         w.tile2(p, t_first + i0, (okm >> i0) & 1ull, (okm >> (i0 + 1)) & 1ull, valid, k0, k1, vb);
       }
     }
-  });
+    if constexpr (st + 1 < kTreeSharedMaxTiles / 2) {
+      if (i0 + 2 < ntile) self(self, std::integral_constant<int, st + 1>{});
+    }
+  };
+  step(step, std::integral_constant<int, 0>{});
   if (active) w.emit(p, nmem - g0, slot0 + g0, G);
 }
 
