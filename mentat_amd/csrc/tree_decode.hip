@@ -99,14 +99,18 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t trsrc(const void* base, int by
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes, 0x00020000);
 }
 
-// LDS geometry of one staged 16-token tile (shared path). K rows are padded
-// by 16 bytes and V rows (16 tokens of one dim) by 8, which makes the MFMA
+// LDS geometry of one stage of the shared path: two 16-token tiles, K of the
+// first, K of the second, then their V as one row of 32 tokens per dim. A V
+// row holds, at positions 8g .. 8g + 3, tokens 4g .. 4g + 3 of the first tile
+// and at 8g + 4 .. 8g + 7 the same tokens of the second: the k index order of
+// the two-tile P.V product, so a lane's V operand is one 16-byte read. K rows
+// are padded by 16 bytes and V rows (64 bytes) by 16, which makes the MFMA
 // operand reads (16 lanes per row group) bank-conflict free.
 template <int D> struct TileLds {
   static constexpr int KRS = 2 * D + 16;
-  static constexpr int VRS = 40;
   static constexpr int KST = 16 * KRS;
-  static constexpr int STAGE = KST + D * VRS;
+  static constexpr int VRS = 80;
+  static constexpr int PAIR = 2 * KST + D * VRS;
 };
 
 // Online-softmax state of one wavefront: 16 query columns (member c/G, head
@@ -145,17 +149,20 @@ struct WaveAttn {
     f32x4_t st = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < KS; ++s) st = TMfma<T>::qk(kr[s], qo[s], st);
-    const int tok0 = t * 16 + 4 * lg;
-    float sc[4];
+    float sc[4];  // raw scores; masked ones -inf
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      sc[i] = st[i] * p.scale_log2;
-      if (!okb || tok0 + i >= valid) sc[i] = kNegInf;
+    for (int i = 0; i < 4; ++i) sc[i] = st[i];
+    if (!(okb && (t + 1) * 16 <= valid)) {  // wave-uniform: only a chunk's last tile is partial
+      const int tok0 = t * 16 + 4 * lg;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (!okb || tok0 + i >= valid) sc[i] = kNegInf;
     }
-    // m is uniform over the four lanes of a column; a lane compares its own
+    // m (log2 units, scale folded in: scale > 0, so the maximum commutes with
+    // it) is uniform over the four lanes of a column; a lane compares its own
     // four scores against it, and only when some lane has outgrown it by the
     // slack is the column maximum formed (cross-lane) and the state rescaled.
-    float pm = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
+    float pm = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])) * p.scale_log2;
     const bool grow = (m == kNegInf) ? (pm != kNegInf) : (pm > m + kTreeSlack);
     if (__builtin_amdgcn_ballot_w64(grow)) {
       pm = fmaxf(pm, __shfl_xor(pm, 16));
@@ -174,7 +181,7 @@ struct WaveAttn {
     const float ms = (m == kNegInf) ? 0.f : m;
     f32x4_t pr;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) pr[i] = fast_exp2(sc[i] - ms);
+    for (int i = 0; i < 4; ++i) pr[i] = fast_exp2(fmaf(sc[i], p.scale_log2, -ms));
     l += (pr[0] + pr[1]) + (pr[2] + pr[3]);  // per-lane partial sum, reduced in emit()
     const uint2 pa = TMfma<T>::pack(pr);
 #pragma unroll
@@ -193,16 +200,22 @@ struct WaveAttn {
       s0 = TMfma<T>::qk(k0[s], qo[s], s0);
       s1 = TMfma<T>::qk(k1[s], qo[s], s1);
     }
-    const int tok0 = t * 16 + 4 * lg;
-    float sc[8];
+    float sc[8];  // raw scores; masked ones -inf
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      sc[i] = s0[i] * p.scale_log2;
-      if (!ok0 || tok0 + i >= valid) sc[i] = kNegInf;
-      sc[4 + i] = s1[i] * p.scale_log2;
-      if (!ok1 || tok0 + 16 + i >= valid) sc[4 + i] = kNegInf;
+      sc[i] = s0[i];
+      sc[4 + i] = s1[i];
     }
-    float pm = fmaxf(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])), fmaxf(fmaxf(sc[4], sc[5]), fmaxf(sc[6], sc[7])));
+    if (!(ok0 && ok1 && (t + 2) * 16 <= valid)) {  // wave-uniform: only a chunk's last step is partial
+      const int tok0 = t * 16 + 4 * lg;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if (!ok0 || tok0 + i >= valid) sc[i] = kNegInf;
+        if (!ok1 || tok0 + 16 + i >= valid) sc[4 + i] = kNegInf;
+      }
+    }
+    float pm = fmaxf(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])), fmaxf(fmaxf(sc[4], sc[5]), fmaxf(sc[6], sc[7]))) *
+               p.scale_log2;
     const bool grow = (m == kNegInf) ? (pm != kNegInf) : (pm > m + kTreeSlack);
     if (__builtin_amdgcn_ballot_w64(grow)) {
       pm = fmaxf(pm, __shfl_xor(pm, 16));
@@ -222,8 +235,8 @@ struct WaveAttn {
     f32x4_t pa, pb;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      pa[i] = fast_exp2(sc[i] - ms);
-      pb[i] = fast_exp2(sc[4 + i] - ms);
+      pa[i] = fast_exp2(fmaf(sc[i], p.scale_log2, -ms));
+      pb[i] = fast_exp2(fmaf(sc[4 + i], p.scale_log2, -ms));
     }
     l += ((pa[0] + pa[1]) + (pa[2] + pa[3])) + ((pb[0] + pb[1]) + (pb[2] + pb[3]));
     const uint2 ua = TMfma<T>::pack(pa), ub = TMfma<T>::pack(pb);
@@ -286,18 +299,25 @@ __device__ __forceinline__ void tree_shared(const TreeParams& p, const int32_t* 
 
   // This thread's 16-byte piece of every tile: waves [0, 2D/64) carry K,
   // waves [2D/64, 4D/64) carry V, the rest carry nothing (D = 64).
+  // A piece lands in LDS as two 8-byte halves, at loff + (tile in stage) *
+  // tstep and hstep bytes apart: contiguous for K; for V (tokens 8h .. 8h + 7
+  // of dim d) at row positions 16h (+ 4 for the stage's second tile) and 8 further.
   const bool loader = wave * 64 < 4 * D;
   const bool is_k = wave * 64 < 2 * D;
-  int goff, loff;
+  int goff, loff, tstep, hstep;
   if (is_k) {
     const int tok = tid / (D / 8), dc = tid % (D / 8);
     goff = (tok * D + dc * 8) * (int)sizeof(S);
     loff = tok * L::KRS + dc * 16;
+    tstep = L::KST;
+    hstep = 8;
   } else {
     const int c = loader ? tid - 2 * D : 0;
     const int d = c >> 1, h = c & 1;
     goff = (d * B + h * 8) * (int)sizeof(S);
-    loff = L::KST + d * L::VRS + h * 16;
+    loff = 2 * L::KST + d * L::VRS + 32 * h;
+    tstep = 8;
+    hstep = 16;
   }
   const S* base = (const S*)(is_k ? p.k : p.v);
   // Tile i of the task (zeros, with no memory traffic, when masked).
@@ -342,18 +362,14 @@ __device__ __forceinline__ void tree_shared(const TreeParams& p, const int32_t* 
         pf[(i0 + kTreePrefetch) % R] = issue(std::integral_constant<int, i0 + kTreePrefetch>{});
       if constexpr (i0 + 1 + kTreePrefetch < kTreeSharedMaxTiles)
         pf[(i0 + 1 + kTreePrefetch) % R] = issue(std::integral_constant<int, i0 + 1 + kTreePrefetch>{});
-      char* stg = lds + (st & 1) * 2 * L::STAGE;
+      char* stg = lds + (st & 1) * L::PAIR;
       if (loader) {
         static_for<2>([&](auto hc) __attribute__((always_inline)) {
           constexpr int h = decltype(hc)::value;
           const uint4 cur = pf[(i0 + h) % R];
-          char* dst = stg + h * L::STAGE + loff;
-          if (is_k) {
-            *(uint4*)__builtin_assume_aligned(dst, 16) = cur;
-          } else {
-            *(uint2*)__builtin_assume_aligned(dst, 8) = make_uint2(cur.x, cur.y);
-            *(uint2*)__builtin_assume_aligned(dst + 8, 8) = make_uint2(cur.z, cur.w);
-          }
+          char* dst = stg + loff + h * tstep;
+          *(uint2*)__builtin_assume_aligned(dst, 8) = make_uint2(cur.x, cur.y);
+          *(uint2*)__builtin_assume_aligned(dst + hstep, 8) = make_uint2(cur.z, cur.w);
         });
       }
       __syncthreads();
@@ -362,15 +378,11 @@ __device__ __forceinline__ void tree_shared(const TreeParams& p, const int32_t* 
 #pragma unroll
         for (int s = 0; s < KS; ++s) {
           k0[s] = *(const uint4*)__builtin_assume_aligned(stg + w.lr * L::KRS + (4 * s + w.lg) * 16, 16);
-          k1[s] = *(const uint4*)__builtin_assume_aligned(stg + L::STAGE + w.lr * L::KRS + (4 * s + w.lg) * 16, 16);
+          k1[s] = *(const uint4*)__builtin_assume_aligned(stg + L::KST + w.lr * L::KRS + (4 * s + w.lg) * 16, 16);
         }
 #pragma unroll
-        for (int j = 0; j < NT; ++j) {
-          const int vo = L::KST + (w.lr + 16 * j) * L::VRS + w.lg * 8;
-          const uint2 a0 = *(const uint2*)__builtin_assume_aligned(stg + vo, 8);
-          const uint2 a1 = *(const uint2*)__builtin_assume_aligned(stg + L::STAGE + vo, 8);
-          vb[j] = make_uint4(a0.x, a0.y, a1.x, a1.y);
-        }
+        for (int j = 0; j < NT; ++j)
+          vb[j] = *(const uint4*)__builtin_assume_aligned(stg + 2 * L::KST + (w.lr + 16 * j) * L::VRS + w.lg * 16, 16);
         w.tile2(p, t_first + i0, (okm >> i0) & 1ull, (okm >> (i0 + 1)) & 1ull, valid, k0, k1, vb);
       }
     }
@@ -439,7 +451,7 @@ __device__ __forceinline__ void tree_solo(const TreeParams& p, const int32_t* it
 
 template <typename T, int D, int G, int B>
 __global__ __launch_bounds__(kTreeThreads) void tree_decode_kernel(TreeParams p) {
-  __shared__ uint4 lds_words[4 * TileLds<D>::STAGE / 16];  // 2 stages x 2 tiles
+  __shared__ uint4 lds_words[2 * TileLds<D>::PAIR / 16];  // 2 stages of 2 tiles
   char* lds = (char*)lds_words;
   const int bid = blockIdx.x;
   if (p.counts) {
@@ -587,6 +599,7 @@ static int tree_decode_call(const void* q, const void* k_store, const void* v_st
       Hq % Hkv != 0 || table_stride <= 0 || num_blocks <= 0 || n_shared < 0 || n_solo < 0 || n_slots < 0)
     return MENTAT_EINVAL;
   if (n_shared + n_solo > 0 && (!items || !members || !q_slots)) return MENTAT_EINVAL;
+  if (!(scale > 0.f) || !std::isfinite(scale)) return MENTAT_EINVAL;  // the kernels fold a positive scale into exp2
   const size_t need = mentat_tree_decode_workspace_bytes(n_slots, Hq, Hkv, D);
   if (need && (!workspace || workspace_bytes < need)) return MENTAT_ESPACE;
   TreeParams p;
