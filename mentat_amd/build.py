@@ -1,5 +1,6 @@
 """Build libmentat_hip.so (gfx950) from mentat_amd/csrc/*.hip with hipcc (and
-the host-only mentat_amd/csrc/*.cpp with the host compiler).
+the host-only mentat_amd/csrc/*.cpp with the host compiler), and the host
+planner extension mentat_amd/_host_plan*.so from mentat_amd/csrc/host_plan.c.
 
 Every call recompiles all sources (objects go to mentat_amd/_build/, the
 library to mentat_amd/lib/libmentat_hip.so). Usage: ``python -m mentat_amd.build``.
@@ -63,6 +64,25 @@ def _compile_host(src: str) -> str:
     return obj
 
 
+# The host planner extension (CPython C API, csrc/host_plan.c) is built in-tree
+# next to the package's modules.
+CC = shutil.which("gcc") or "gcc"
+
+
+def build_host_ext(verbose: bool = True) -> str:
+    import sysconfig
+
+    src = os.path.join(CSRC, "host_plan.c")
+    out = os.path.join(HERE, "_host_plan" + sysconfig.get_config_var("EXT_SUFFIX"))
+    tmp = out + ".tmp"
+    _run([CC, "-O2", "-shared", "-fPIC", "-Wall", "-Wextra", "-Wno-unused-parameter",
+          "-I", sysconfig.get_paths()["include"], src, "-o", tmp])
+    os.replace(tmp, out)
+    if verbose:
+        print(f"built {out}", file=sys.stderr)
+    return out
+
+
 def build(verbose: bool = True) -> str:
     os.makedirs(BUILD, exist_ok=True)
     os.makedirs(LIBDIR, exist_ok=True)
@@ -80,6 +100,7 @@ def build(verbose: bool = True) -> str:
     os.replace(tmp, LIB)
     if verbose:
         print(f"built {LIB} from {len(srcs)} sources", file=sys.stderr)
+    build_host_ext(verbose)
     return LIB
 
 

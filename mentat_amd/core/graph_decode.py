@@ -58,7 +58,7 @@ import gc
 import numpy as np
 import torch
 
-from .. import ops
+from .. import ops, tree_plan
 from .._lib import LAYOUT_NATIVE, get_lib
 from ..adapters.model_adapter import _HFDecoderAdapter
 
@@ -145,16 +145,18 @@ SPLIT_LAYERS = 2
 TREE_DECODE = True
 
 
-def _tree_caps(nb: int, Hkv: int, max_len: int) -> tuple:
+def _tree_caps(nb: int, Hkv: int, max_len: int, G: int) -> tuple:
     """(max_shared, max_solo, max_slots) of a bucket's plan buffers. A plan
     without sharing (each query one segment, solo items of 4 tiles) needs at
     most nb * ceil(tiles / 4) * Hkv items and slots; a query cut into k
     segments adds at most k - 1 chunks, and k <= 9 is allowed before the
-    planner falls back to that plan. Shared tasks (segments of >= 9 queries)
-    need one item per 32 tiles per head per 32 queries."""
+    planner falls back to that plan. Shared tasks (segments of at least
+    min_q queries: SHARED_MIN_GROUPS groups of 16 / G) need one item per 32
+    tiles per head per 32 queries."""
     tiles = -(-max_len // 16)
-    solo = nb * (-(-tiles // 4) + 8) * Hkv
-    shared = max(1, -(-nb // 9)) * (-(-tiles // 32) + 2) * Hkv * 2
+    solo = nb * (-(-tiles // tree_plan.CHUNK_TILES) + 8) * Hkv
+    min_q = (tree_plan.SHARED_MIN_GROUPS - 1) * (16 // G) + 1
+    shared = max(1, -(-nb // min_q)) * (-(-tiles // tree_plan.SHARED_CHUNK_TILES) + 2) * Hkv * 2
     return shared, solo, solo
 
 
@@ -354,7 +356,7 @@ class DecodeGraphs:
         nbytes = lib.mentat_paged_decode_workspace_bytes(m.layout, self.max_batch, Hq, Hkv, D, m.block_size,
                                                          m._pages_cap * m.block_size, 0, 0)
         if self.tree:
-            slots = _tree_caps(self.max_batch, Hkv, m._pages_cap * m.block_size)[2]
+            slots = _tree_caps(self.max_batch, Hkv, m._pages_cap * m.block_size, self.G)[2]
             nbytes = max(nbytes, lib.mentat_tree_decode_workspace_bytes(slots, Hq, Hkv, D))
         if self._ws is not None and self._ws.numel() >= nbytes:
             return
@@ -378,7 +380,7 @@ class DecodeGraphs:
         b.dev.copy_(b.host)
         b.tree = None
         if self.tree:  # zero-filled: no items, every query's output zero, until a plan is written
-            caps = _tree_caps(nb, self.a.num_key_value_heads, m._pages_cap * m.block_size)
+            caps = _tree_caps(nb, self.a.num_key_value_heads, m._pages_cap * m.block_size, self.G)
             b.tree = ops.TreePlanBuffers(self.dev, nb, self.a.num_key_value_heads, *caps)
             # recorded after each replay of the graph that reads the plan: the
             # next plan's copy waits for it
@@ -435,10 +437,11 @@ class DecodeGraphs:
             self._graphs.clear()
         m = self.m
         L = m.num_layers
-        offsets = [m.get_kv_length(s) for s in seq_ids]  # RoPE positions: lengths before the append
-        rows = [m._sequences[s].row for s in seq_ids]
         k = self._split_layers()
         st = m.plan_append_step_begin(seq_ids, max(k, 1))
+        p0 = st["plan"][0]   # layer 0's plan: table rows, and lengths after the append
+        rows = p0[3]
+        lens = p0[5]
         # Overlap the later layers' planning with the first graph only when every
         # layer's counters agree: then every layer's new token lands on the same
         # page index, so the first layers' plan decides the table capacity.
@@ -453,7 +456,7 @@ class DecodeGraphs:
         h = b.host_np
         plans_h = h[3 * nb:].reshape(L, 7, nb)
         h[0:n] = token_ids
-        h[nb:nb + n] = offsets
+        h[nb:nb + n] = lens - 1   # RoPE positions: lengths before the append
         h[2 * nb:2 * nb + n] = rows
         self._fill_padding(h, nb, n)
         if overlap:
@@ -463,7 +466,7 @@ class DecodeGraphs:
             b.graph.replay()
             # while the first graph runs: the tree plan (layer 0's tables are
             # final), then the later layers' appends
-            self._plan_tree(b, seq_ids, rows)
+            self._plan_tree(b, rows, lens)
             plan = m.plan_append_step_finish(st)
             if int(plan[k:, 4].max()) >= m._pages_cap:
                 raise RuntimeError("DecodeGraphs: a later layer's append needs more table pages than the first")
@@ -476,7 +479,7 @@ class DecodeGraphs:
         else:
             plans_h[:, :, :n] = plan
             b.dev.copy_(b.host, non_blocking=True)
-            self._plan_tree(b, seq_ids, rows)
+            self._plan_tree(b, rows, lens)
             b.copied.record()
             b.graph.replay()
             if b.graph2 is not None:
@@ -485,18 +488,15 @@ class DecodeGraphs:
                 b.tree_read.record()
         return b.logits[:n].clone(), b.hidden[:n].clone()
 
-    def _plan_tree(self, b: _Bucket, seq_ids: list, rows: list) -> None:
+    def _plan_tree(self, b: _Bucket, rows: np.ndarray, lens: np.ndarray) -> None:
         """The step's prefix-tree plan (after layer 0's appends are planned:
-        the tables and lengths attention reads) into the bucket's buffers, and
-        their copy to the device queued."""
+        the tables and lengths attention reads; rows and lens are the batch's
+        table rows and lengths after the append) into the bucket's buffers,
+        and their copy to the device queued."""
         if b.tree is None:
             return
         m = self.m
-        seqs = m._sequences
-        n = len(seq_ids)
-        lens = np.fromiter((seqs[s].num_tokens[0] for s in seq_ids), dtype=np.int32, count=n)
-        _, _, _, shared = b.tree.plan(m.host_tables0(), np.asarray(rows, dtype=np.int32), lens, m.block_size,
-                                      self.G)
+        _, _, _, shared = b.tree.plan(m.host_tables0(), rows, lens, m.block_size, self.G)
         if shared:
             self.tree_steps += 1
         else:

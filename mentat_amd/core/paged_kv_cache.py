@@ -39,6 +39,11 @@ import torch
 from .. import ops
 from .._lib import LAYOUT_NATIVE, LAYOUT_REFERENCE
 
+try:  # the host planner in C (mentat_amd/csrc/host_plan.c): the same steps on the same objects
+    from .. import _host_plan
+except ImportError:  # not built: the Python planner below
+    _host_plan = None
+
 __all__ = ["BlockAllocator", "SequenceState", "PagedKVCacheManager", "PagedKVView"]
 
 
@@ -370,9 +375,44 @@ class PagedKVCacheManager:
             self._host_t0_row(seq)
         return plan
 
+    def _native_plan(self) -> bool:
+        return _host_plan is not None and type(self.allocator) is BlockAllocator
+
+    def _mirror_t0(self, plan0: np.ndarray) -> None:
+        """Layer 0's planned table entries into the host copy of its tables."""
+        self._widen_host_t0(int(plan0[4].max()) + 1)
+        self._host_t0[plan0[3], plan0[4]] = plan0[0]
+
     def plan_append_batched(self, seq_ids: list[int], layer_idx: int) -> np.ndarray:
         """Host half of ``append_tokens_batched`` (one token per sequence, in
-        batch order): returns the int32 [7, N] plan."""
+        batch order): returns the int32 [7, N] plan. Rows: destination block,
+        slot, copy-on-write source (-1: none), table row, page index, new
+        length, batch index."""
+        if layer_idx != 0 or not seq_ids:
+            return self._plan_batched(seq_ids, layer_idx)
+        try:
+            return self._plan_batched(seq_ids, 0)
+        except Exception:
+            self._resync_t0(seq_ids)
+            raise
+
+    def _resync_t0(self, seq_ids) -> None:
+        """Layer 0's rows of the host copy from the page tables (after a plan
+        that failed part-way, e.g. out of blocks, left some tables grown)."""
+        for sid in seq_ids:
+            seq = self._sequences.get(sid)
+            if seq is not None and seq.row >= 0:
+                self._host_t0_row(seq)
+
+    def _plan_batched(self, seq_ids: list[int], layer_idx: int) -> np.ndarray:
+        if seq_ids and self._native_plan():
+            plan = np.empty((7, len(seq_ids)), dtype=np.int32)
+            seqs = self._sequences
+            if _host_plan.append_batched([seqs[s] for s in seq_ids], layer_idx, self.block_size, self.allocator,
+                                         plan) is not None:
+                if layer_idx == 0:
+                    self._mirror_t0(plan)
+                return plan
         B = self.block_size
         alloc = self.allocator
         rc = alloc.refcounts
@@ -406,8 +446,7 @@ class PagedKVCacheManager:
         plan = np.array([dst, slots, cows, rows, pages, lens, list(range(len(seq_ids)))],
                         dtype=np.int32).reshape(7, len(seq_ids))
         if L == 0 and seq_ids:
-            self._widen_host_t0(int(plan[4].max()) + 1)
-            self._host_t0[plan[3], plan[4]] = plan[0]
+            self._mirror_t0(plan)
         return plan
 
     def plan_append_step(self, seq_ids: list[int]) -> np.ndarray:
@@ -439,6 +478,18 @@ class PagedKVCacheManager:
         if N == 0:
             return st
         seqs = [self._sequences[s] for s in seq_ids]
+        upto = min(max(first_layers, 1), L)
+        if self._native_plan():
+            try:
+                r = _host_plan.step_begin(seqs, L, self.block_size, self.allocator, plan)
+            except Exception:
+                self._resync_t0(seq_ids)
+                raise
+            if r is not None:  # the C planner: layer 0, then layers 1 .. upto - 1
+                self._mirror_t0(plan[0])
+                st.update(seqs=seqs, native=r[0], uniform=r[1], next=1)
+                self._plan_layers(st, upto)
+                return st
         rc = self.allocator.refcounts
         # Every layer's counters equal layer 0's (else every layer is planned on its own).
         uniform = all(s.num_tokens.count(s.num_tokens[0]) == L
@@ -456,7 +507,7 @@ class PagedKVCacheManager:
         st.update(seqs=seqs, pts=pts, uniform=uniform, paged=paged, tails0=tails0, rc0=rc0,
                   shared0=any(r > 1 for r in rc0), ngroups0=len(set(tails0)), p0=p0,
                   events=sorted([(i, 0) for i in new_at] + [(i, 1) for i in cow_at]), next=1)
-        self._plan_layers(st, min(max(first_layers, 1), L))
+        self._plan_layers(st, upto)
         return st
 
     def plan_append_step_finish(self, st: dict) -> np.ndarray:
@@ -477,6 +528,10 @@ class PagedKVCacheManager:
         if l0 >= upto:
             return
         st["next"] = upto
+        if "native" in st:
+            _host_plan.step_layers(st["native"], l0, upto, self.num_layers, self.block_size, self.allocator,
+                                   st["plan"])
+            return
         plan, seqs, pts, rc = st["plan"], st["seqs"], st["pts"], self.allocator.refcounts
         tails0, rc0, p0, events = st["tails0"], st["rc0"], st["p0"], st["events"]
         alloc, release = self.allocator.alloc, self.allocator.release

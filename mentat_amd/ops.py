@@ -24,6 +24,7 @@ from ._lib import (
     ptr,
     stream_handle,
 )
+from . import tree_plan
 
 __all__ = [
     "paged_decode",
@@ -627,7 +628,8 @@ class TreePlanBuffers:
                 self.dev[lo:lo + slots].copy_(self.host[lo:lo + slots], non_blocking=True)
 
     def plan(self, tables: np.ndarray, qrows: np.ndarray, lens: np.ndarray, block_size: int, G: int,
-             chunk_tiles: int = 4, shared_chunk_tiles: int = 32, shared_min_groups: int = 3) -> tuple:
+             chunk_tiles: int = tree_plan.CHUNK_TILES, shared_chunk_tiles: int = tree_plan.SHARED_CHUNK_TILES,
+             shared_min_groups: int = tree_plan.SHARED_MIN_GROUPS) -> tuple:
         """Plan n queries with the native planner (mentat_tree_plan) straight
         into the host twin. tables: host int32 [rows, stride] block ids indexed
         by table row; qrows, lens: int32 per query. When a capacity is exceeded

@@ -38,6 +38,11 @@ import numpy as np
 ITEM_FIELDS = 8
 WAVES_PER_WG = 8
 SHARED_MAX_TILES = 32  # tiles per shared task (the kernel's unrolled tile loop)
+# Default plan: solo items of 4 tiles, shared tasks of up to 32 tiles for chunks of
+# at least 2 member groups (measured best at the prefix-tree and rollout shapes)
+CHUNK_TILES = 4
+SHARED_CHUNK_TILES = 32
+SHARED_MIN_GROUPS = 2
 
 
 @dataclass
@@ -240,7 +245,8 @@ def _items_of(sg: SegmentArrays, sel: np.ndarray, B: int, Hkv: int, chunk: int, 
 
 
 def build_plan(tables, lens, rows, *, block_size: int, Hkv: int, G: int,
-               chunk_tiles: int = 4, shared_chunk_tiles: int = 32, shared_min_groups: int = 3) -> TreePlan:
+               chunk_tiles: int = CHUNK_TILES, shared_chunk_tiles: int = SHARED_CHUNK_TILES,
+               shared_min_groups: int = SHARED_MIN_GROUPS) -> TreePlan:
     """Segments -> shared tasks, solo items and per-(query, head) partial slots.
 
     ``tables``: the queries' page tables (lists, or an int32 [N, P] array whose

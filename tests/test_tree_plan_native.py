@@ -71,12 +71,14 @@ def test_native_plan_without_sharing_and_capacity():
     B, Hkv, G = 16, 8, 4
     tables, lens, rows, mirror = _batch(5, 4, 100, 12, 60, B)
     uniq = [[10000 * i + b for b in t] for i, t in enumerate(tables)]      # no ids in common
-    want = build_plan(uniq, lens, rows, block_size=B, Hkv=Hkv, G=G)
+    want = build_plan(uniq, lens, rows, block_size=B, Hkv=Hkv, G=G, chunk_tiles=4, shared_chunk_tiles=32,
+                      shared_min_groups=3)
     st, counts, items, members, off, qs = _native(mirror, rows, lens, B, Hkv, G, 4, 32, 3, share=0)
     assert st == 0 and counts.tolist() == [0, want.n_solo, want.n_slots]
     assert np.array_equal(items[:want.items.shape[0] * 8].reshape(-1, 8), want.items)
     assert np.array_equal(off, want.q_slot_offsets)
-    full = build_plan(tables, lens, rows, block_size=B, Hkv=Hkv, G=G)
+    full = build_plan(tables, lens, rows, block_size=B, Hkv=Hkv, G=G, chunk_tiles=4, shared_chunk_tiles=32,
+                      shared_min_groups=3)
     assert full.n_shared > 0 and full.n_solo > 0
     for caps in ((full.n_shared - 1, 10 ** 6, 10 ** 6), (10 ** 6, full.n_solo - 1, 10 ** 6),
                  (10 ** 6, 10 ** 6, full.n_slots - 1)):
