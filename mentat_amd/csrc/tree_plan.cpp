@@ -14,7 +14,8 @@
 // Items (int32 x 8, the kernel's layout): table row, first tile, tile count,
 // valid tokens, kv head, member count, first slot, member offset. Shared tasks
 // (segments of >= shared_min_groups groups of 16/G queries) come first, in
-// chunks of shared_chunk_tiles tiles and member sets of 8 * 16/G; then solo
+// chunks of shared_chunk_tiles tiles and member sets of 8 * 16/G, longest
+// (most tiles) first and otherwise in the order below; then solo
 // items in chunks of chunk_tiles tiles and sets of 16/G; both chunk-major,
 // then kv head, then member set. Member j of an item writes slot first + j;
 // q_slots lists each (query, head)'s slots in slot order.
@@ -87,11 +88,16 @@ extern "C" int mentat_tree_plan(const int32_t* tables, int64_t table_stride, con
   }
   const int mg = 16 / G;
   int n_items[2] = {0, 0}, n_slots = 0;
-  // pass 0: shared tasks, pass 1: solo items
+  // pass 0: shared tasks (collected, then longest first: a stable sort by tile
+  // count, so the kernel's queue starts the longest ones first), pass 1: solo items
+  struct Rec {
+    int row, c0, nt, end, h, mc, m0;
+  };
+  std::vector<Rec> recs;
   for (int pass = 0; pass < 2; ++pass) {
     const int chunk = pass == 0 ? shared_chunk_tiles : chunk_tiles;
     const int cap = pass == 0 ? kWavesPerTask * mg : mg;
-    const int max_items = pass == 0 ? max_shared : max_solo;
+    recs.clear();
     for (const Seg& s : segs) {
       const bool shared = (s.count + mg - 1) / mg >= shared_min_groups;
       if (shared != (pass == 0)) continue;
@@ -100,19 +106,22 @@ extern "C" int mentat_tree_plan(const int32_t* tables, int64_t table_stride, con
       const int row = qrows[s.owner];
       for (int c0 = t0; c0 < t1; c0 += chunk) {
         const int nt = std::min(chunk, t1 - c0);
-        for (int h = 0; h < Hkv; ++h) {
-          for (int k0 = 0; k0 < s.count; k0 += cap) {
-            const int mc = std::min(cap, s.count - k0);
-            if (n_items[pass] >= max_items || n_slots + mc > max_slots) return MENTAT_ESPACE;
-            int32_t* it = items + (int64_t)(pass == 0 ? n_items[0] : max_shared + n_items[1]) * kFields;
-            it[0] = row; it[1] = c0; it[2] = nt; it[3] = end; it[4] = h; it[5] = mc; it[6] = n_slots;
-            it[7] = n_slots;
-            for (int m = 0; m < mc; ++m) members[n_slots + m] = s.owner + k0 + m;
-            ++n_items[pass];
-            n_slots += mc;
-          }
-        }
+        for (int h = 0; h < Hkv; ++h)
+          for (int k0 = 0; k0 < s.count; k0 += cap) recs.push_back({row, c0, nt, end, h, std::min(cap, s.count - k0),
+                                                                   s.owner + k0});
       }
+    }
+    if (pass == 0)
+      std::stable_sort(recs.begin(), recs.end(), [](const Rec& a, const Rec& b) { return a.nt > b.nt; });
+    const int max_items = pass == 0 ? max_shared : max_solo;
+    for (const Rec& r : recs) {
+      if (n_items[pass] >= max_items || n_slots + r.mc > max_slots) return MENTAT_ESPACE;
+      int32_t* it = items + (int64_t)(pass == 0 ? n_items[0] : max_shared + n_items[1]) * kFields;
+      it[0] = r.row; it[1] = r.c0; it[2] = r.nt; it[3] = r.end; it[4] = r.h; it[5] = r.mc; it[6] = n_slots;
+      it[7] = n_slots;
+      for (int m = 0; m < r.mc; ++m) members[n_slots + m] = r.m0 + m;
+      ++n_items[pass];
+      n_slots += r.mc;
     }
   }
   // Solo items follow the shared tasks directly.

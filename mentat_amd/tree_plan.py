@@ -261,6 +261,8 @@ def build_plan(tables, lens, rows, *, block_size: int, Hkv: int, G: int,
     groups = (sg.count + mg - 1) // mg
     shared = groups >= shared_min_groups
     a_sh, m_sh = _items_of(sg, np.nonzero(shared)[0], block_size, Hkv, shared_chunk_tiles, WAVES_PER_WG * mg)
+    order = np.argsort(-a_sh[:, 2], kind="stable")   # shared tasks longest first (the kernel's queue order)
+    a_sh, m_sh = a_sh[order], m_sh[order]
     a_so, m_so = _items_of(sg, np.nonzero(~shared)[0], block_size, Hkv, chunk_tiles, mg)
     body = np.concatenate([a_sh, a_so])
     m_start = np.concatenate([m_sh, m_so])
