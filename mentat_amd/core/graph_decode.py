@@ -38,10 +38,10 @@ captured layer also fuses that glue: each residual add with the RMSNorm that
 follows it (across the layer boundary too), RoPE of Q and K in one launch, and
 SiLU(gate) * up (ops.rmsnorm, ops.rope_, ops.silu_mul); other models run their
 modules as they are. Without QK-norm (Llama) the q/k/v projections also run
-as one GEMM and gate/up as another: each layer's weights are concatenated once
-and the modules' own weights become views into the merged tensors (no second
-copy; the eager path reads the same storage). If a module's weight is later
-rebound (e.g. ``model.to``), the next step merges again and recaptures.
+as one GEMM and gate/up as another, over per-layer concatenated copies of the
+modules' weights (the modules are left as they are); each step refreshes a
+copy's rows from any module weight that was rebound or changed in place
+since (MERGE_PROJECTIONS selects this, views instead of copies, or no merge).
 
 No object is destroyed while a capture is active: the garbage collector runs
 just before each capture and stays disabled during it. (A finished run's
@@ -117,9 +117,20 @@ def _mergeable(a) -> bool:
     return True
 
 
+# How the captured Llama step gets its merged q/k/v and gate/up weights:
+# "copy" (default): its own concatenated copies, the modules untouched; every
+# step compares each module's weight (the tensor and its in-place version
+# counter) with the one copied and refreshes the copy's rows in place when it
+# changed (layers of the first graph before it starts, the others while it
+# runs). "views": the modules' weights become views of one concatenated tensor
+# per layer (no second copy; a rebound weight is merged again and the graphs
+# captured again). "off": separate q/k/v and gate/up GEMMs.
+MERGE_PROJECTIONS = "copy"
+
+
 def _merge_linears(lins) -> torch.Tensor:
     """One weight [sum(out), in] for the bias-free linears ``lins``; each
-    module's weight becomes a view of its rows."""
+    module's weight becomes a view of its rows ("views" mode)."""
     w = torch.cat([lin.weight.detach() for lin in lins], dim=0)
     off = 0
     for lin in lins:
@@ -178,9 +189,11 @@ class DecodeGraphs:
         self._ws = None
         self.captures = 0
         self.fused = _fusable(self.a, self.m.dtype)
-        self.merged = self.fused and _mergeable(self.a)
+        self.merge_mode = MERGE_PROJECTIONS
+        self.merged = self.fused and self.merge_mode in ("copy", "views") and _mergeable(self.a)
         self._w_qkv: list = []
         self._w_gu: list = []
+        self._w_src: list = []   # "copy": per layer [module params dict, tensor, data_ptr, version, merged, row]
         if self.merged:
             self._merge()
         Hq, Hkv = self.a.num_attention_heads, self.a.num_key_value_heads
@@ -194,13 +207,32 @@ class DecodeGraphs:
         self.max_batch = self.buckets[-1]
 
     def _merge(self) -> None:
+        groups = lambda b: ((b.self_attn.q_proj, b.self_attn.k_proj, b.self_attn.v_proj),  # noqa: E731
+                            (b.mlp.gate_proj, b.mlp.up_proj))
         with torch.no_grad():
-            self._w_qkv = [_merge_linears((b.self_attn.q_proj, b.self_attn.k_proj, b.self_attn.v_proj))
-                           for b in self.a.layers]
-            self._w_gu = [_merge_linears((b.mlp.gate_proj, b.mlp.up_proj)) for b in self.a.layers]
+            if self.merge_mode == "views":
+                self._w_qkv = [_merge_linears(groups(b)[0]) for b in self.a.layers]
+                self._w_gu = [_merge_linears(groups(b)[1]) for b in self.a.layers]
+                return
+            self._w_qkv, self._w_gu, self._w_src = [], [], []
+            for b in self.a.layers:
+                recs = []
+                for lins, dst in zip(groups(b), (self._w_qkv, self._w_gu)):
+                    w = torch.cat([lin.weight.detach() for lin in lins], dim=0)
+                    dst.append(w)
+                    row = 0
+                    for lin in lins:
+                        t = lin._parameters["weight"]
+                        recs.append([lin._parameters, t, t.data_ptr(), t._version, w, row])
+                        row += t.shape[0]
+                self._w_src.append(recs)
 
     def _merged_current(self) -> bool:
-        """The modules' weights still view the merged tensors (first and last layer)."""
+        """The merged weights can serve this step: "copy" always (they are
+        refreshed); "views": the modules' weights still view the merged tensors
+        (first and last layer)."""
+        if self.merge_mode != "views":
+            return True
         layers = self.a.layers
         for i in (0, len(layers) - 1):
             b = layers[i]
@@ -208,6 +240,25 @@ class DecodeGraphs:
                     or b.mlp.gate_proj.weight.data_ptr() != self._w_gu[i].data_ptr()):
                 return False
         return True
+
+    def _refresh(self, lo: int, hi: int) -> None:
+        """"copy" mode: layers lo .. hi - 1 of the merged copies take the rows of
+        any module weight rebound or changed in place since it was copied (in
+        stream order, before the graph that reads them). A weight whose shape
+        changed cannot be copied in place: ValueError."""
+        if not self._w_src:
+            return
+        for recs in self._w_src[lo:hi]:
+            for r in recs:
+                t = r[0]["weight"]
+                if t is r[1] and t._version == r[3] and t.data_ptr() == r[2]:
+                    continue
+                w, row = r[4], r[5]
+                if t.shape[0] != r[1].shape[0] or t.shape[1:] != w.shape[1:] or t.dtype != w.dtype:
+                    raise ValueError("DecodeGraphs: a merged projection weight changed shape or dtype")
+                with torch.no_grad():
+                    w[row:row + t.shape[0]].copy_(t.detach())
+                r[1], r[2], r[3] = t, t.data_ptr(), t._version
 
     # ------------------------------------------------------------------
     def bucket(self, n: int):
@@ -433,7 +484,7 @@ class DecodeGraphs:
         if nb is None:
             return None
         if self.merged and not self._merged_current():
-            self._merge()           # weights were rebound: merge again, capture again
+            self._merge()           # ("views") weights were rebound: merge again, capture again
             self._graphs.clear()
         m = self.m
         L = m.num_layers
@@ -463,11 +514,13 @@ class DecodeGraphs:
             cut = 3 * nb + k * 7 * nb
             plans_h[:k, :, :n] = plan[:k]
             b.dev[:cut].copy_(b.host[:cut], non_blocking=True)
+            self._refresh(0, k)
             b.graph.replay()
             # while the first graph runs: the tree plan (layer 0's tables are
-            # final), then the later layers' appends
+            # final), the later layers' appends and merged weights
             self._plan_tree(b, rows, lens)
             plan = m.plan_append_step_finish(st)
+            self._refresh(k, L)
             if int(plan[k:, 4].max()) >= m._pages_cap:
                 raise RuntimeError("DecodeGraphs: a later layer's append needs more table pages than the first")
             plans_h[k:, :, :n] = plan[k:]
@@ -481,6 +534,7 @@ class DecodeGraphs:
             b.dev.copy_(b.host, non_blocking=True)
             self._plan_tree(b, rows, lens)
             b.copied.record()
+            self._refresh(0, L)
             b.graph.replay()
             if b.graph2 is not None:
                 b.graph2.replay()

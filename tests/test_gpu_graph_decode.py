@@ -245,13 +245,18 @@ def test_no_garbage_collection_during_capture(gpu, monkeypatch, split):
     assert gc.isenabled()
 
 
-def test_rebound_weights_are_merged_again(gpu):
-    """The captured Llama step runs q/k/v and gate/up as merged GEMMs over views of
-    the modules' weights; rebinding a weight (a new tensor) is detected on the next
-    step, which merges again and recaptures, so its logits follow the new weights."""
-    print("case merged projections after a weight rebind", flush=True)
+def test_merged_projections_leave_the_model_alone_and_follow_its_weights(gpu):
+    """The captured Llama step runs q/k/v and gate/up as merged GEMMs over its own
+    copies of the modules' weights: the modules keep their tensors, and a weight
+    rebound (a new tensor) or changed in place is picked up by the next step,
+    whose logits follow the new weights (no recapture: the copies are refreshed
+    in place)."""
+    print("case merged projections after a weight rebind and an in-place change", flush=True)
     model = _bf16_model()
+    before = [(b.self_attn.q_proj.weight.data_ptr(), b.mlp.up_proj.weight.data_ptr()) for b in model.model.layers]
     we, wg = _wrapper(model, False), _wrapper(model, True)
+    assert [(b.self_attn.q_proj.weight.data_ptr(), b.mlp.up_proj.weight.data_ptr())
+            for b in model.model.layers] == before
     with torch.no_grad():
         ids = torch.tensor([[3, 1, 4, 1, 5, 9, 2, 6]], device="cuda")
         se, sg = we.kv_cache_mgr.allocate_sequence(), wg.kv_cache_mgr.allocate_sequence()
@@ -267,5 +272,11 @@ def test_rebound_weights_are_merged_again(gpu):
             b.mlp.gate_proj.weight.data = (b.mlp.gate_proj.weight.data * 0.5).clone()
         le, _ = we.decode_batch_tensor([8], [se])
         lg, _ = wg.decode_batch_tensor([8], [sg])
-        assert wg.graphs.captures > n0
         assert float((lg.float() - le.float()).abs().max()) <= 2e-2 * float(le.float().abs().max()) + 2e-2
+        for b in model.model.layers:  # in place, the same tensors
+            b.self_attn.v_proj.weight.mul_(-1.0)
+            b.mlp.up_proj.weight.mul_(0.75)
+        le, _ = we.decode_batch_tensor([9], [se])
+        lg, _ = wg.decode_batch_tensor([9], [sg])
+        assert float((lg.float() - le.float()).abs().max()) <= 2e-2 * float(le.float().abs().max()) + 2e-2
+        assert wg.graphs.captures == n0
