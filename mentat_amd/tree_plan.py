@@ -120,8 +120,14 @@ class TreePlan:
         mem = self.members
         if mem.dtype != np.int32 or mem.ndim != 1:
             raise ValueError("members must be int32 [n]")
+        # Items with tiles write their members' slots; padding items (no tiles)
+        # are skipped by the kernel and must have no members.
+        if np.any((it[:, 2] <= 0) & (it[:, 5] != 0)):
+            raise ValueError("an item with members has no tiles: its slots would never be written")
         live = it[:, 2] > 0
         if not live.any():
+            if off[-1]:
+                raise ValueError("q_slot_offsets lists slots that no item writes")
             return
         a = it[live]
         mg = 16 // G
@@ -144,6 +150,12 @@ class TreePlan:
         idx = np.repeat(a[:, 7].astype(np.int64) - np.cumsum(a[:, 5]) + a[:, 5], a[:, 5]) + np.arange(tot)
         if np.any((mem[idx] < 0) | (mem[idx] >= Nq)):
             raise ValueError("member query index out of range")
+        # The merge reads the slots q_slot_offsets lists per (query, head): as
+        # many as the items write for it (with slots in range and each written
+        # once, the merge then reads exactly the written ones).
+        keys = mem[idx].astype(np.int64) * Hkv + np.repeat(a[:, 4], a[:, 5])
+        if not np.array_equal(np.bincount(keys, minlength=Nq * Hkv), np.diff(off.astype(np.int64))):
+            raise ValueError("q_slot_offsets does not count the slots the items write per (query, head)")
 
     def device_arrays(self, device) -> tuple:
         """(items, members, q_slot_offsets, q_slots) as int32 device tensors (uploaded once)."""

@@ -7,6 +7,8 @@ distinct (block, valid tokens) pages, and a float64 evaluation that follows the
 plan item by item (partial softmax per item, log-sum-exp merge per query)
 must equal the oracle's per-sequence attention.
 """
+import dataclasses
+
 import numpy as np
 import pytest
 import torch
@@ -134,6 +136,36 @@ def test_plan_items_and_slots(min_groups):
         for q in plan.members[a[7]: a[7] + a[5]]:
             cover[q, a[4]] += toks
     assert (cover == np.array(lens)[:, None]).all()
+
+
+def test_validate_requires_slot_counts_to_match_the_items():
+    """The merge reads the slots q_slot_offsets lists for each (query, head):
+    validate rejects plans whose items write a different number of slots for
+    a unit, and items with members but no tiles (the kernel skips those, so
+    their slots would hold stale partials)."""
+    m, _, ids, tables, lens, rows = _host_trees(1)
+    Hkv, G = 8, 4
+    args = (len(ids), Hkv, G, max(rows) + 1, max(len(t) for t in tables), 16)
+    plan = build_plan(tables, lens, rows, block_size=16, Hkv=Hkv, G=G)
+    plan.validate(*args)
+    # a member moved to another query: two units' counts no longer match
+    it = plan.items[plan.n_shared]
+    moved = plan.members.copy()
+    moved[it[7]] = (moved[it[7]] + 1) % len(ids)
+    bad = dataclasses.replace(plan, members=moved)
+    with pytest.raises(ValueError, match="count the slots"):
+        bad.validate(*args)
+    # an item with members but no tiles
+    zero = plan.items.copy()
+    zero[plan.n_shared, 2] = 0
+    with pytest.raises(ValueError, match="has no tiles"):
+        dataclasses.replace(plan, items=zero).validate(*args)
+    # a padding item (no tiles, no members) while its slots stay listed
+    pad = plan.items.copy()
+    pad[plan.n_shared, 2] = 0
+    pad[plan.n_shared, 5] = 0
+    with pytest.raises(ValueError, match="count the slots"):
+        dataclasses.replace(plan, items=pad).validate(*args)
 
 
 def _plan_eval_f64(q, kp, vp, tables, rows, plan, B, scale):
