@@ -310,6 +310,20 @@ int mentat_kv_append(int layout, const void* k_new, const void* v_new, void* k_p
                      int64_t num_blocks, int dtype, int32_t* block_tables, int64_t table_stride,
                      int64_t table_rows, int32_t* seq_lens, void* stream);
 
+/* mentat_rope_qkv followed by mentat_kv_append of its k and v, in one launch
+ * (bf16/f16): rotated q goes to the dense q [rows][Hq][D]; for each plan column
+ * the rotated k and the v of source row plan[6] (< rows) are written straight
+ * into the pools (K/V heads Hk) at the column's (block, slot), with that
+ * column's copy-on-write and table / length update. Pools, tables, lengths and
+ * q hold the same bits as the two calls. Replaces, for one decode step's layer,
+ * the adapters' RoPE of q and k (adapters/llama_adapter.py:70-113) and the
+ * device half of append_tokens_batched (core/paged_kv_cache.py:227-284). */
+int mentat_rope_qkv_append(int layout, const void* qkv, int64_t row_stride, void* q, const void* cos,
+                           const void* sin, int rows, int Hq, int Hk, int D, void* k_pool, void* v_pool,
+                           const int32_t* plan, int n, int block_size, int64_t num_blocks, int dtype,
+                           int32_t* block_tables, int64_t table_stride, int64_t table_rows, int32_t* seq_lens,
+                           void* stream);
+
 /* Batched whole-page copy dst[i] <- src[i] in each of n_pools pools (e.g. the
  * K and V pools of every layer in one launch). `pools` is a DEVICE array of
  * n_pools base pointers; block_bytes = bytes of one page. Pairs with an

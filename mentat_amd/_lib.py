@@ -148,6 +148,15 @@ SIGNATURES: dict[str, tuple] = {
             _c_void_p,  # stream
         ],
     ),
+    "mentat_rope_qkv_append": (
+        _c_int,
+        [
+            _c_int, _c_void_p, _c_i64, _c_void_p, _c_void_p, _c_void_p,  # layout, qkv, row_stride, q, cos, sin
+            _c_int, _c_int, _c_int, _c_int, _c_void_p, _c_void_p,  # rows, Hq, Hk, D, k_pool, v_pool
+            _c_void_p, _c_int, _c_int, _c_i64, _c_int,  # plan, n, block_size, num_blocks, dtype
+            _c_void_p, _c_i64, _c_i64, _c_void_p, _c_void_p,  # tables, stride, table rows, lens, stream
+        ],
+    ),
     "mentat_page_copy": (
         _c_int,
         [_c_void_p, _c_int, _c_void_p, _c_void_p, _c_int, _c_i64, _c_i64, _c_void_p],

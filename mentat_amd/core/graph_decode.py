@@ -367,19 +367,27 @@ class DecodeGraphs:
         for layer_idx in range(lo, hi):
             block = layers[layer_idx]
             attn = a.get_self_attn(block)
-            if self.merged:
+            if self.merged and m.dtype == x.dtype:
                 qkv = torch.nn.functional.linear(x, self._w_qkv[layer_idx])  # [1, nb, (Hq + 2 Hk) * D]
                 cos, sin = a._build_cos_sin(pos, qkv)
-                q, k, v = ops.rope_qkv(qkv, Hq, Hk, cos, sin)               # dense [nb, H, D]
+                # RoPE of q and k with k and v written straight into the pages
+                q = ops.rope_qkv_append(qkv, Hq, Hk, cos, sin, m._k_store, m._v_store, plans[layer_idx],
+                                        block_size=m.block_size, layout=m.layout,
+                                        block_tables=m._tables[layer_idx], seq_lens=m._lens[layer_idx])
             else:
-                q, k, v = a.project_qkv(attn, x.squeeze(0).unsqueeze(1))  # one token per sequence
-                cos, sin = a._build_cos_sin(pos, q)
-                q, k = q.contiguous(), k.contiguous()
-                ops.rope_(q, k, cos, sin)
-                q, k, v = q.squeeze(1), k.squeeze(1), v.squeeze(1)
-            ops.kv_append(k.to(m.dtype).contiguous(), v.to(m.dtype).contiguous(),
-                          m._k_store, m._v_store, plans[layer_idx], block_size=m.block_size, layout=m.layout,
-                          block_tables=m._tables[layer_idx], seq_lens=m._lens[layer_idx])
+                if self.merged:
+                    qkv = torch.nn.functional.linear(x, self._w_qkv[layer_idx])
+                    cos, sin = a._build_cos_sin(pos, qkv)
+                    q, k, v = ops.rope_qkv(qkv, Hq, Hk, cos, sin)           # dense [nb, H, D]
+                else:
+                    q, k, v = a.project_qkv(attn, x.squeeze(0).unsqueeze(1))  # one token per sequence
+                    cos, sin = a._build_cos_sin(pos, q)
+                    q, k = q.contiguous(), k.contiguous()
+                    ops.rope_(q, k, cos, sin)
+                    q, k, v = q.squeeze(1), k.squeeze(1), v.squeeze(1)
+                ops.kv_append(k.to(m.dtype).contiguous(), v.to(m.dtype).contiguous(),
+                              m._k_store, m._v_store, plans[layer_idx], block_size=m.block_size, layout=m.layout,
+                              block_tables=m._tables[layer_idx], seq_lens=m._lens[layer_idx])
             o = self._attention(q.contiguous(), layer_idx, rows, max_seqlen, tree)
             attn_out = attn.o_proj(o.reshape(1, nb, -1))
             ln = block.post_attention_layernorm

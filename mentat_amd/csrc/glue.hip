@@ -19,28 +19,6 @@ namespace mentat {
 
 namespace {
 
-template <typename T> struct G16;
-template <> struct G16<BF16> {
-  __device__ static float lo(uint32_t w) { return bf16_lo(w); }
-  __device__ static float hi(uint32_t w) { return bf16_hi(w); }
-  __device__ static uint32_t bits(float v) { return f32_to_bf16(v); }
-  __device__ static float rnd(float v) { return __uint_as_float((uint32_t)f32_to_bf16(v) << 16); }
-};
-// The empty asm makes the float value exist before it is narrowed (no fused
-// mixed-precision instruction that would round once).
-template <> struct G16<F16> {
-  __device__ static float lo(uint32_t w) { return f16_bits_to_f32((uint16_t)(w & 0xffffu)); }
-  __device__ static float hi(uint32_t w) { return f16_bits_to_f32((uint16_t)(w >> 16)); }
-  __device__ static uint32_t bits(float v) {
-    asm volatile("" : "+v"(v));
-    return f32_to_f16_bits(v);
-  }
-  __device__ static float rnd(float v) {
-    asm volatile("" : "+v"(v));
-    return f16_bits_to_f32(f32_to_f16_bits(v));
-  }
-};
-
 constexpr int kNormThreads = 256;
 
 // One workgroup per row; each thread owns 8-element groups g = tid, tid + 256, ...
@@ -174,8 +152,8 @@ __global__ __launch_bounds__(256) void rope_kernel(const uint16_t* qi, uint16_t*
   const uint16_t* c = cs + (long)row * D;
   const uint16_t* s = sn + (long)row * D;
   const float a = ld(src, i), b = ld(src, i + half);
-  const float ya = E::rnd(E::rnd(a * ld(c, i)) + E::rnd(-b * ld(s, i)));
-  const float yb = E::rnd(E::rnd(b * ld(c, i + half)) + E::rnd(a * ld(s, i + half)));
+  float ya, yb;
+  rope_pair<T>(a, b, ld(c, i), ld(s, i), ld(c, i + half), ld(s, i + half), ya, yb);
   dst[i] = (uint16_t)E::bits(ya);
   dst[i + half] = (uint16_t)E::bits(yb);
 }

@@ -104,6 +104,42 @@ template <> struct Elem<F16> {
   __device__ static void store1(void* p, long i, float v) { ((uint16_t*)p)[i] = f32_to_f16_bits(v); }
 };
 
+// 16-bit values as torch's elementwise kernels round them: lo/hi unpack a
+// packed pair, rnd rounds an fp32 result to the dtype (one rounding per torch
+// op), bits gives the rounded value's 16 bits.
+template <typename T> struct G16;
+template <> struct G16<BF16> {
+  __device__ static float lo(uint32_t w) { return bf16_lo(w); }
+  __device__ static float hi(uint32_t w) { return bf16_hi(w); }
+  __device__ static uint32_t bits(float v) { return f32_to_bf16(v); }
+  __device__ static float rnd(float v) { return __uint_as_float((uint32_t)f32_to_bf16(v) << 16); }
+};
+// The empty asm makes the float value exist before it is narrowed (no fused
+// mixed-precision instruction that would round once).
+template <> struct G16<F16> {
+  __device__ static float lo(uint32_t w) { return f16_bits_to_f32((uint16_t)(w & 0xffffu)); }
+  __device__ static float hi(uint32_t w) { return f16_bits_to_f32((uint16_t)(w >> 16)); }
+  __device__ static uint32_t bits(float v) {
+    asm volatile("" : "+v"(v));
+    return f32_to_f16_bits(v);
+  }
+  __device__ static float rnd(float v) {
+    asm volatile("" : "+v"(v));
+    return f16_bits_to_f32(f32_to_f16_bits(v));
+  }
+};
+
+// RoPE of one (a, b) = (t[i], t[i + D/2]) pair as the adapters' torch code
+// rounds it, t' = rnd(rnd(t * cos) + rnd(rotate_half(t) * sin)):
+// a' = rnd(rnd(a c_i) + rnd(-b s_i)), b' = rnd(rnd(b c_{i+D/2}) + rnd(a s_{i+D/2})).
+template <typename T>
+__device__ __forceinline__ void rope_pair(float a, float b, float ci, float si, float ch, float sh, float& ya,
+                                          float& yb) {
+  using E = G16<T>;
+  ya = E::rnd(E::rnd(a * ci) + E::rnd(-b * si));
+  yb = E::rnd(E::rnd(b * ch) + E::rnd(a * sh));
+}
+
 // ---- 16-byte dot products: q (kept in its packed form) · k -----------------------------
 // For 16-bit types the packed pairs go straight into v_dot2 (fp32 accumulate).
 template <typename T> struct Dot16;

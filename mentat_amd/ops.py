@@ -303,6 +303,67 @@ def rope_qkv(qkv: torch.Tensor, Hq: int, Hk: int, cos: torch.Tensor, sin: torch.
     return q, k, v
 
 
+def rope_qkv_append(
+    qkv: torch.Tensor,
+    Hq: int,
+    Hk: int,
+    cos: torch.Tensor,
+    sin: torch.Tensor,
+    k_store: torch.Tensor,
+    v_store: torch.Tensor,
+    plan: torch.Tensor,
+    *,
+    block_size: int,
+    layout: int = LAYOUT_REFERENCE,
+    block_tables: Optional[torch.Tensor] = None,
+    seq_lens: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """:func:`rope_qkv` followed by :func:`kv_append` of its k and v in one
+    launch (mentat_rope_qkv_append): returns the rotated q [rows, Hq, D]; the
+    rotated k and the v of each plan column's source row go straight into the
+    stores (same bits as the two calls)."""
+    _require(qkv.dtype in _GLUE_DTYPES and cos.dtype == qkv.dtype and sin.dtype == qkv.dtype,
+             "rope_qkv_append takes bf16/f16 tensors of one dtype")
+    _require(cos.is_contiguous() and sin.is_contiguous(), "dense cos / sin rows required")
+    D = cos.shape[-1]
+    rows = cos.numel() // D
+    W = (Hq + 2 * Hk) * D
+    _require(qkv.shape[-1] == W and qkv.numel() == rows * W and qkv.is_contiguous(),
+             "qkv must be contiguous [rows, (Hq + 2 Hk) * D]")
+    dev = qkv.device
+    _require(k_store.device == dev and v_store.device == dev, "qkv and the stores must share a device")
+    _require(k_store.dtype == qkv.dtype and v_store.dtype == qkv.dtype, "store dtype differs from qkv")
+    _require(k_store.is_contiguous() and v_store.is_contiguous(), "stores must be contiguous")
+    _require(plan.dim() == 2 and plan.shape[0] == len(PLAN_FIELDS), "plan must be int32 [7, n]")
+    _check_i32(plan, "plan", dev)
+    _check_i32(block_tables, "block_tables", dev)
+    _check_i32(seq_lens, "seq_lens", dev)
+    num_blocks = k_store.shape[0]
+    if layout == LAYOUT_NATIVE:
+        _require(tuple(k_store.shape) == (num_blocks, Hk, block_size, D), "bad native K store")
+        _require(tuple(v_store.shape) == (num_blocks, Hk, D, block_size), "bad native V store")
+    else:
+        _require(tuple(k_store.shape) == (num_blocks, block_size, Hk, D), "bad K pool")
+        _require(tuple(v_store.shape) == (num_blocks, block_size, Hk, D), "bad V pool")
+    trows = stride = 0
+    if block_tables is not None:
+        _require(block_tables.dim() == 2, "block_tables must be [rows, stride]")
+        trows, stride = block_tables.shape
+        _require(block_tables.stride(0) == stride, "block_tables rows must be dense")
+        if seq_lens is not None:
+            _require(seq_lens.numel() >= trows, "seq_lens shorter than block_tables")
+    elif seq_lens is not None:
+        trows = seq_lens.numel()
+    q = torch.empty(rows, Hq, D, dtype=qkv.dtype, device=dev)
+    st = get_lib().mentat_rope_qkv_append(
+        layout, ptr(qkv), W, ptr(q), ptr(cos), ptr(sin), rows, Hq, Hk, D, ptr(k_store), ptr(v_store), ptr(plan),
+        plan.shape[1], block_size, num_blocks, DTYPE_CODES[qkv.dtype], ptr(block_tables), stride, trows,
+        ptr(seq_lens), stream_handle(dev),
+    )
+    check(st, "mentat_rope_qkv_append")
+    return q
+
+
 def silu_mul(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
     """silu(gate) * up with torch's rounding per op (mentat_silu_mul)."""
     _require(gate.dtype in _GLUE_DTYPES and up.dtype == gate.dtype and up.shape == gate.shape,

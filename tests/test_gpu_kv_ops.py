@@ -140,3 +140,46 @@ def test_table_copy_rows(gpu):
     exp_l[:, 5] = l0[:, 1]
     exp_l[:, 6] = l0[:, 4]
     assert torch.equal(tables, exp_t) and torch.equal(lens, exp_l)
+
+
+@pytest.mark.parametrize("layout", [LAYOUT_REFERENCE, LAYOUT_NATIVE])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_rope_qkv_append_equals_rope_qkv_then_kv_append(gpu, layout, dtype):
+    """One launch, the same bits: q, both pools, the tables and the lengths
+    equal those of rope_qkv followed by kv_append of its k and v, for a decode
+    plan (copy-on-write of shared tails, a padding column with no destination,
+    more q rows than plan columns, source rows out of order) and a prefill plan
+    (21 tokens over a copied tail page and a fresh page)."""
+    decode = np.array([
+        [20, 10, 21, 23, 30, 22, -1],   # dst block (-1: padding column)
+        [5, 5, 0, 0, 7, 15, 0],         # slot
+        [10, -1, -1, 11, -1, 12, -1],   # cow source
+        [0, 1, 2, 3, 4, 5, -1],         # row
+        [2, 2, 3, 0, 1, 4, 0],          # page
+        [38, 38, 49, 1, 24, 80, -1],    # new length
+        [3, 0, 8, 1, 5, 2, 7],          # source row
+    ], dtype=np.int32)
+    n = 21
+    prefill = np.array([[40] * 7 + [41] * 14, list(range(9, 16)) + list(range(0, 14)), [3] + [-1] * 20, [2] * n,
+                        [0] * 7 + [1] * 14, [-1] * (n - 1) + [30], list(range(n))], dtype=np.int32)
+    for name, plan, rows, Hq, Hk, D in (("decode", decode, 9, 32, 8, 128), ("prefill", prefill, n, 8, 2, 64)):
+        print(f"case rope_qkv_append {name} layout={layout} {dtype}", flush=True)
+        nb, B = 64, 16
+        g = torch.Generator(device=gpu).manual_seed(11)
+        qkv = torch.randn(1, rows, (Hq + 2 * Hk) * D, generator=g, device=gpu).to(dtype)
+        cos = (2 * torch.rand(1, rows, 1, D, generator=g, device=gpu) - 1).to(dtype)
+        sin = (2 * torch.rand(1, rows, 1, D, generator=g, device=gpu) - 1).to(dtype)
+        ks, vs = _stores(layout, nb, B, Hk, D, dtype, gpu, 3)
+        tables = torch.randint(0, nb, (8, 6), dtype=torch.int32, device=gpu)
+        lens = torch.randint(0, 100, (8,), dtype=torch.int32, device=gpu)
+        ks2, vs2, tables2, lens2 = ks.clone(), vs.clone(), tables.clone(), lens.clone()
+        p = torch.from_numpy(plan).to(gpu)
+        q, k, v = ops.rope_qkv(qkv, Hq, Hk, cos, sin)
+        ops.kv_append(k, v, ks, vs, p, block_size=B, layout=layout, block_tables=tables, seq_lens=lens)
+        q2 = ops.rope_qkv_append(qkv, Hq, Hk, cos, sin, ks2, vs2, p, block_size=B, layout=layout,
+                                 block_tables=tables2, seq_lens=lens2)
+        torch.cuda.synchronize()
+        assert torch.equal(q2, q)
+        assert torch.equal(ks2, ks) and torch.equal(vs2, vs)
+        assert torch.equal(tables2, tables) and torch.equal(lens2, lens)
+        assert not torch.equal(ks2, _stores(layout, nb, B, Hk, D, dtype, gpu, 3)[0])  # something was written
