@@ -193,13 +193,16 @@ class PagedModelWrapper:
         self.config = model.config
         self.graphs = None
 
-    def enable_step_capture(self) -> None:
+    def enable_step_capture(self, buckets=None) -> None:
         """Run batched decode steps as captured graph replays (core/graph_decode.py);
-        batches above its largest bucket still run eagerly."""
+        batches above its largest bucket still run eagerly. ``buckets``: the batch
+        sizes to capture (default: the tables measured on an MI355X), or
+        "calibrate" to measure this device's table first
+        (DecodeGraphs.calibrate_buckets; also MENTAT_CALIBRATE_BUCKETS=1)."""
         from .graph_decode import DecodeGraphs
 
         if self.graphs is None:
-            self.graphs = DecodeGraphs(self)
+            self.graphs = DecodeGraphs(self, buckets=buckets)
 
     @torch.no_grad()
     def prefill(self, input_ids: torch.LongTensor, seq_id: int) -> torch.Tensor:

@@ -42,6 +42,12 @@ as one GEMM and gate/up as another, over per-layer concatenated copies of the
 modules' weights (the modules are left as they are); each step refreshes a
 copy's rows from any module weight that was rebound or changed in place
 since (MERGE_PROJECTIONS selects this, views instead of copies, or no merge).
+The RoPE of the merged q/k/v output then also writes k and v straight into
+the pages (ops.rope_qkv_append: RoPE and KV append in one launch).
+
+The batch-size buckets are tables measured on an MI355X (BUCKETS,
+MERGED_BUCKETS); ``buckets="calibrate"`` measures this device's table instead
+(DecodeGraphs.calibrate_buckets).
 
 No object is destroyed while a capture is active: the garbage collector runs
 just before each capture and stays disabled during it. (A finished run's
@@ -54,6 +60,7 @@ freed by reference counting, outside any capture.
 from __future__ import annotations
 
 import gc
+import os
 
 import numpy as np
 import torch
@@ -201,10 +208,64 @@ class DecodeGraphs:
         self.tree = bool(TREE_DECODE and self.m.layout == LAYOUT_NATIVE and self.G and 16 % self.G == 0)
         self.tree_steps = 0       # steps whose plan shared pages
         self.tree_fallbacks = 0   # steps planned without sharing (a capacity was exceeded)
-        if buckets is None:
+        self.bucket_costs: dict = {}
+        if buckets is None and os.environ.get("MENTAT_CALIBRATE_BUCKETS", "") == "1":
+            buckets = "calibrate"
+        if isinstance(buckets, str):
+            if buckets != "calibrate":
+                raise ValueError(f"buckets must be row counts or 'calibrate', got {buckets!r}")
+            buckets = self.calibrate_buckets()
+        elif buckets is None:
             buckets = MERGED_BUCKETS if self.merged else BUCKETS
         self.buckets = tuple(sorted(buckets))
         self.max_batch = self.buckets[-1]
+
+    @torch.no_grad()
+    def calibrate_buckets(self, max_batch: int = 256, step: int = 8, reps: int = 3, tol: float = 0.01) -> tuple:
+        """A bucket table measured on this device for this model. The step's
+        projection GEMMs as the captured step runs them (merged q/k/v and
+        gate/up when it merges them, o and down, every layer, and the LM head)
+        are timed at each multiple of ``step`` rows up to ``max_batch``; a row
+        count is kept unless some larger one costs at most (1 + tol) times as
+        much (a batch then runs in that larger bucket at about the same cost).
+        BUCKETS / MERGED_BUCKETS were found this way on one MI355X; the GEMM
+        library's kernel choice, and with it the cheap row counts, can differ
+        with the device and the library version. The timings stay in
+        ``bucket_costs`` (ms per step's projections, by row count)."""
+        a = self.a
+        mats = []
+        for i, b in enumerate(a.layers):
+            attn, mlp = a.get_self_attn(b), a.get_mlp(b)
+            if self.merged:
+                mats += [self._w_qkv[i], attn.o_proj.weight, self._w_gu[i], mlp.down_proj.weight]
+            else:
+                mats += [attn.q_proj.weight, attn.k_proj.weight, attn.v_proj.weight, attn.o_proj.weight,
+                         mlp.gate_proj.weight, mlp.up_proj.weight, mlp.down_proj.weight]
+        mats.append(a.lm_head.weight)
+        g = torch.Generator(device=self.dev).manual_seed(0)
+        xs = {}
+        for w in mats:
+            if w.shape[1] not in xs:
+                xs[w.shape[1]] = torch.randn(max_batch, w.shape[1], generator=g, device=self.dev).to(w.dtype)
+
+        def projections(r):
+            for w in mats:
+                torch.nn.functional.linear(xs[w.shape[1]][:r], w)
+
+        cost = {}
+        for r in range(step, max_batch + 1, step):
+            projections(r)   # the library's first call at a shape picks its kernel
+            t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            t0.record()
+            for _ in range(reps):
+                projections(r)
+            t1.record()
+            t1.synchronize()
+            cost[r] = t0.elapsed_time(t1) / reps
+        rs = sorted(cost)
+        keep = tuple(r for i, r in enumerate(rs) if all(cost[r2] > (1 + tol) * cost[r] for r2 in rs[i + 1:]))
+        self.bucket_costs = cost
+        return keep
 
     def _merge(self) -> None:
         groups = lambda b: ((b.self_attn.q_proj, b.self_attn.k_proj, b.self_attn.v_proj),  # noqa: E731

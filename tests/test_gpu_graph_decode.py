@@ -280,3 +280,41 @@ def test_merged_projections_leave_the_model_alone_and_follow_its_weights(gpu):
         lg, _ = wg.decode_batch_tensor([9], [sg])
         assert float((lg.float() - le.float()).abs().max()) <= 2e-2 * float(le.float().abs().max()) + 2e-2
         assert wg.graphs.captures == n0
+
+
+def test_calibrated_buckets(gpu):
+    """buckets="calibrate": the table comes from timings of the step's own
+    projection GEMMs on this device at every multiple of 8 rows up to 256. It
+    is sorted, ends at 256, and each kept row count is cheaper by more than 1%
+    than every larger one. Captured steps on that table match eager steps."""
+    print("case calibrated buckets, bf16 2-layer llama", flush=True)
+    model = _bf16_model()
+    we, wg = _wrapper(model, False), _wrapper(model, False)
+    wg.enable_step_capture(buckets="calibrate")
+    g = wg.graphs
+    b, c = g.buckets, g.bucket_costs
+    assert b == tuple(sorted(b)) and b[-1] == 256 and all(r % 8 == 0 for r in b)
+    assert sorted(c) == list(range(8, 257, 8)) and all(v > 0 for v in c.values())
+    for r in b:
+        assert all(c[r2] > 1.01 * c[r] for r2 in c if r2 > r), r
+    rng = np.random.default_rng(1)
+    live = []
+    with torch.no_grad():
+        for p in range(2):
+            ids = torch.tensor([rng.integers(0, 4096, 30 + 7 * p).tolist()], device="cuda")
+            se, sg = we.kv_cache_mgr.allocate_sequence(), wg.kv_cache_mgr.allocate_sequence()
+            we.prefill(ids, se)
+            wg.prefill(ids, sg)
+            live.append(se)
+        for parent in list(live):
+            c1 = we.kv_cache_mgr.fork_sequence(parent)
+            assert wg.kv_cache_mgr.fork_sequence(parent) == c1
+            live.append(c1)
+        toks = [1] * len(live)
+        for _ in range(3):
+            le, _ = we.decode_batch_tensor(toks, live)
+            lg, _ = wg.decode_batch_tensor(toks, live)
+            scale = float(le.float().abs().max())
+            assert float((lg.float() - le.float()).abs().max()) <= 2e-2 * scale + 2e-2
+            toks = le.float().argmax(-1).tolist()
+    assert g.captures >= 1 and g.bucket(len(live)) in b
