@@ -50,7 +50,8 @@ MERGED_BUCKETS); ``buckets="calibrate"`` measures this device's table instead
 (DecodeGraphs.calibrate_buckets).
 
 No object is destroyed while a capture is active: the garbage collector runs
-just before each capture and stays disabled during it. (A finished run's
+before the captures (once for all the buckets ``prepare`` captures, else just
+before the capture) and stays disabled during each capture. (A finished run's
 graphs, pools and pinned buffers, if left to the cyclic collector, could
 otherwise be torn down in the middle of another capture, where the HIP calls
 of that teardown are not allowed and abort the process.) This object also
@@ -195,6 +196,7 @@ class DecodeGraphs:
         self._copy_stream = torch.cuda.Stream(self.dev)  # tree plan copies, overlapping the first graph
         self._ws = None
         self.captures = 0
+        self._warm_full = True   # the next capture warms up with the whole forward
         self.fused = _fusable(self.a, self.m.dtype)
         self.merge_mode = MERGE_PROJECTIONS
         self.merged = self.fused and self.merge_mode in ("copy", "views") and _mergeable(self.a)
@@ -220,6 +222,33 @@ class DecodeGraphs:
         self.buckets = tuple(sorted(buckets))
         self.max_batch = self.buckets[-1]
 
+    def _projection_weights(self) -> list:
+        """The weights of the step's projection GEMMs, in step order: per layer
+        q/k/v (merged when the step merges them), o, gate/up (likewise) and
+        down, then the LM head."""
+        a = self.a
+        mats = []
+        for i, b in enumerate(a.layers):
+            attn, mlp = a.get_self_attn(b), a.get_mlp(b)
+            if self.merged:
+                mats += [self._w_qkv[i], attn.o_proj.weight, self._w_gu[i], mlp.down_proj.weight]
+            else:
+                mats += [attn.q_proj.weight, attn.k_proj.weight, attn.v_proj.weight, attn.o_proj.weight,
+                         mlp.gate_proj.weight, mlp.up_proj.weight, mlp.down_proj.weight]
+        mats.append(a.lm_head.weight)
+        return mats
+
+    @torch.no_grad()
+    def _warm_gemms(self, nb: int) -> None:
+        """One call of each distinct projection GEMM shape at nb rows: the GEMM
+        library picks (and loads) its kernels for these shapes outside capture."""
+        seen = set()
+        for w in self._projection_weights():
+            key = (tuple(w.shape), w.dtype)
+            if key not in seen:
+                seen.add(key)
+                torch.nn.functional.linear(torch.zeros(nb, w.shape[1], dtype=w.dtype, device=self.dev), w)
+
     @torch.no_grad()
     def calibrate_buckets(self, max_batch: int = 256, step: int = 8, reps: int = 3, tol: float = 0.01) -> tuple:
         """A bucket table measured on this device for this model. The step's
@@ -232,16 +261,7 @@ class DecodeGraphs:
         library's kernel choice, and with it the cheap row counts, can differ
         with the device and the library version. The timings stay in
         ``bucket_costs`` (ms per step's projections, by row count)."""
-        a = self.a
-        mats = []
-        for i, b in enumerate(a.layers):
-            attn, mlp = a.get_self_attn(b), a.get_mlp(b)
-            if self.merged:
-                mats += [self._w_qkv[i], attn.o_proj.weight, self._w_gu[i], mlp.down_proj.weight]
-            else:
-                mats += [attn.q_proj.weight, attn.k_proj.weight, attn.v_proj.weight, attn.o_proj.weight,
-                         mlp.gate_proj.weight, mlp.up_proj.weight, mlp.down_proj.weight]
-        mats.append(a.lm_head.weight)
+        mats = self._projection_weights()
         g = torch.Generator(device=self.dev).manual_seed(0)
         xs = {}
         for w in mats:
@@ -335,9 +355,10 @@ class DecodeGraphs:
         m = self.m
         m.reserve(rows, -(-max_len // m.block_size))
         top = self.bucket(min(max_batch, self.max_batch))
+        gc.collect()   # once for all of them (a full collection costs ~0.1 s at Llama-8B size)
         for b in self.buckets:
             if b <= top:
-                self._get(b)
+                self._get(b, collect=False)
 
     # ------------------------------------------------------------------
     def _inputs_layout(self, nb: int):
@@ -483,7 +504,7 @@ class DecodeGraphs:
         with torch.cuda.stream(self._stream):
             self._ws = ops.workspace(self.dev, nbytes)
 
-    def _get(self, nb: int) -> _Bucket:
+    def _get(self, nb: int, collect: bool = True) -> _Bucket:
         b = self._graphs.get(nb)
         if b is not None and b.version == self.m.tables_version:
             return b
@@ -513,14 +534,23 @@ class DecodeGraphs:
         s = self._stream
         s.wait_stream(torch.cuda.current_stream(self.dev))
         with torch.cuda.stream(s):
-            for _ in range(2):  # warm-up (library handles, GEMM selection) on all-padding input
+            # Warm-up outside capture on all-padding input. The first capture runs
+            # the whole forward (library handles, every kernel's first launch);
+            # later ones only meet new GEMM shapes (every other kernel of the
+            # step runs the same code at any batch size), so they warm the
+            # projection GEMMs at this row count.
+            # (The GEMM-only warm-up needs the fused step's HF module layout.)
+            if self._warm_full or not self.fused:
                 self._forward(b.dev, nb, tree=b.tree)
+            else:
+                self._warm_gemms(nb)
         torch.cuda.current_stream(self.dev).wait_stream(s)
         g = torch.cuda.CUDAGraph()
         g2 = None
         k = self._split_layers()
         gc_on = gc.isenabled()
-        gc.collect()
+        if collect:
+            gc.collect()
         gc.disable()
         try:
             if k:
@@ -538,6 +568,7 @@ class DecodeGraphs:
                 gc.enable()
         torch.cuda.current_stream(self.dev).wait_stream(s)
         b.graph, b.graph2 = g, g2
+        self._warm_full = False
         b.version = m.tables_version
         self._graphs[nb] = b
         self.captures += 1
