@@ -319,11 +319,226 @@ __global__ __launch_bounds__(kPfThreads) void prefill_attn_kernel(PrefillParams 
   });
 }
 
+// ---- head_dim 128: 32 query columns per wavefront on v_mfma_f32_32x32x16 ----
+// Per 32-key step a wavefront computes S^T[32 keys x 32 query columns] =
+// K.Q^T (8 MFMAs over 16-dim blocks; A = K rows from LDS, B = the column's q in
+// registers) and O^T[128 dims x 32 columns] += V^T.P^T (2 key chunks x 4 dim
+// blocks). Each K/V operand read from LDS thus feeds 32 columns, twice the
+// 16-column kernel's, which is LDS-bound at one tile per wavefront. Lane l owns
+// column l % 32; its 16 accumulator values of S^T are keys 8(r/4) + 4(l/32) +
+// r%4 of the step (r < 16), the other 16 keys of the column sit in lane l ^ 32,
+// so the column's running maximum takes one exchange and the O rescale none.
+// P^T as the B operand of chunk c is the lane's values r = 8c .. 8c+7 as they
+// are: MFMA k index 8(l/32) + e is key 16c + 8(e/4) + 4(l/32) + e%4, and the
+// A operand V^T reads exactly those keys of its dim (two 8-byte LDS reads).
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+template <typename T> struct PMfma32;
+template <> struct PMfma32<BF16> {
+  __device__ static f32x16_t mma(const uint4& a, const uint4& b, f32x16_t c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b),
+                                                   c, 0, 0, 0);
+  }
+  __device__ static uint32_t bits(float v) { return f32_to_bf16(v); }
+};
+template <> struct PMfma32<F16> {
+  __device__ static f32x16_t mma(const uint4& a, const uint4& b, f32x16_t c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, a), __builtin_bit_cast(f16x8_t, b),
+                                                  c, 0, 0, 0);
+  }
+  __device__ static uint32_t bits(float v) { return f32_to_f16_bits(v); }
+};
+
+constexpr int kP32Waves = 4;
+constexpr int kP32Threads = 64 * kP32Waves;
+constexpr int kP32Rows = 32 * kP32Waves;  // query rows per workgroup
+
+template <typename T, int G>
+__global__ __launch_bounds__(kP32Threads) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void prefill_attn32_kernel(PrefillParams p) {
+  using S = typename T::storage;
+  constexpr int D = 128;
+  using L = PfLds<D>;
+  using M = PMfma32<T>;
+  constexpr int CH = D / 8;        // 16-byte chunks per token row
+  constexpr int NQ = kPfKeys / 4;  // token quads per stage
+  static_assert(NQ * CH == kP32Threads, "one (token quad, chunk) per thread and stage");
+  __shared__ __attribute__((aligned(16))) char lds[2 * L::STAGE];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int n = lane & 31, h = lane >> 5;
+  const int rows = p.S * G;
+  const int rb = (int)(gridDim.x - 1 - blockIdx.x);  // later row blocks (more keys) start first
+  const int hk = blockIdx.y, b = blockIdx.z;
+  const int r0 = rb * kP32Rows;
+  const int pos_lo = r0 / G;
+  const int pos_hi = min(p.S - 1, (r0 + kP32Rows - 1) / G);
+  const int key_lo = p.window > 0 ? max(0, pos_lo - p.window + 1) : 0;
+  const int t_lo = key_lo / kPfKeys, t_hi = pos_hi / kPfKeys;
+
+  // This wavefront's columns: rows rw .. rw + 31 (position row / G, head row % G).
+  const int rw = r0 + 32 * wave;
+  const int tpos_hi = rw < rows ? min((rw + 31) / G, p.S - 1) : -1;
+  const int tkey_lo = p.window > 0 ? min(rw / G, p.S - 1) - p.window + 1 : 0;
+  const int tpos_lo = rw / G;
+  const int tkmin_hi = p.window > 0 ? tpos_hi - p.window + 1 : 0;
+  const bool tfull = rw + 31 < rows;
+  const int row = rw + n;
+  const bool col_ok = row < rows;
+  const int qpos = col_ok ? row / G : 0;
+  const int kmin = p.window > 0 ? qpos - p.window + 1 : 0;
+  const int qhead = hk * G + (col_ok ? row % G : 0);
+  uint4 qo[D / 16];  // B operand of dim block s: dims 16s + 8h .. 16s + 8h + 7 of the column
+  {
+    const S* qp = (const S*)p.q + (((long)b * p.S + qpos) * p.Hq + qhead) * D + 8 * h;
+#pragma unroll
+    for (int s2 = 0; s2 < D / 16; ++s2) {
+      const uint4 w = *(const uint4*)(qp + 16 * s2);
+      qo[s2] = col_ok ? w : make_uint4(0, 0, 0, 0);
+    }
+  }
+  f32x16_t o[D / 32];
+#pragma unroll
+  for (int j = 0; j < D / 32; ++j) o[j] = f32x16_t{};
+  float m = kNegInf, l = 0.f;
+
+  // Staging as in prefill_attn_kernel: thread tid moves tokens 4tq .. 4tq+3, dims
+  // 8lc .. 8lc+7 of K and V (V written transposed).
+  const int tq = tid / CH, lc = tid - (tid / CH) * CH;
+  uint4 kw[4], vw[4];
+  auto gload = [&](int t) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int tok = t * kPfKeys + 4 * tq + u;
+      const int tc = min(tok, p.S - 1);
+      const long off = (((long)b * p.S + tc) * p.Hkv + hk) * D + 8 * lc;
+      kw[u] = *(const uint4*)((const S*)p.k + off);
+      vw[u] = *(const uint4*)((const S*)p.v + off);
+      if (tok >= p.S) { kw[u] = make_uint4(0, 0, 0, 0); vw[u] = make_uint4(0, 0, 0, 0); }
+    }
+  };
+  auto lstore = [&](int stage) {
+    char* st = lds + stage * L::STAGE;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) *(uint4*)(st + (4 * tq + u) * L::KRS + lc * 16) = kw[u];
+    const uint32_t* w0 = (const uint32_t*)&vw[0];
+    const uint32_t* w1 = (const uint32_t*)&vw[1];
+    const uint32_t* w2 = (const uint32_t*)&vw[2];
+    const uint32_t* w3 = (const uint32_t*)&vw[3];
+    char* vt = st + L::KST + 8 * tq;
+#pragma unroll
+    for (int hh = 0; hh < 4; ++hh) {
+      const uint2 lo = make_uint2(__builtin_amdgcn_perm(w1[hh], w0[hh], 0x05040100u),
+                                  __builtin_amdgcn_perm(w3[hh], w2[hh], 0x05040100u));
+      const uint2 hi = make_uint2(__builtin_amdgcn_perm(w1[hh], w0[hh], 0x07060302u),
+                                  __builtin_amdgcn_perm(w3[hh], w2[hh], 0x07060302u));
+      *(uint2*)(vt + (8 * lc + 2 * hh) * L::VRS) = lo;
+      *(uint2*)(vt + (8 * lc + 2 * hh + 1) * L::VRS) = hi;
+    }
+  };
+
+  gload(t_lo);
+  lstore(0);
+  __syncthreads();
+  for (int t = t_lo; t <= t_hi; ++t) {
+    const int stage = (t - t_lo) & 1;
+    const bool more = t < t_hi;
+    gload(min(t + 1, t_hi));  // the last iteration reloads its own stage and stores nothing
+    const char* st = lds + stage * L::STAGE;
+#pragma unroll
+    for (int h2 = 0; h2 < kPfKeys / 32; ++h2) {
+      const int kb = t * kPfKeys + 32 * h2;  // first key of this step
+      if (!(kb <= tpos_hi && kb + 31 >= tkey_lo)) continue;  // wave-uniform: no column sees these keys
+      const char* ks = st + (32 * h2 + n) * L::KRS + 16 * h;
+      f32x16_t sa = f32x16_t{};
+#pragma unroll
+      for (int s2 = 0; s2 < D / 16; ++s2) sa = M::mma(*(const uint4*)(ks + 32 * s2), qo[s2], sa);
+      float sc[16];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) sc[r] = sa[r];
+      const bool inside = tfull && kb + 31 <= tpos_lo && kb >= tkmin_hi;
+      if (!inside) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int key = kb + 8 * (r / 4) + 4 * h + (r % 4);
+          if (!col_ok || key > qpos || key < kmin) sc[r] = kNegInf;
+        }
+      }
+      float pm = sc[0];
+#pragma unroll
+      for (int r = 1; r < 16; ++r) pm = fmaxf(pm, sc[r]);
+      pm = fmaxf(pm, __shfl_xor(pm, 32));  // the column's other 16 keys
+      pm = pm == kNegInf ? kNegInf : pm * p.scale_log2;
+      const bool grow = (m == kNegInf) ? (pm != kNegInf) : (pm > m + kPfSlack);
+      if (__builtin_amdgcn_ballot_w64(grow)) {
+        const float mn = fmaxf(m, pm);
+        const float alpha = (mn == kNegInf) ? 1.f : fast_exp2(m - mn);
+        l *= alpha;
+        m = mn;
+#pragma unroll
+        for (int j = 0; j < D / 32; ++j) o[j] *= alpha;
+      }
+      const float ms = (m == kNegInf) ? 0.f : m;
+      float pr[16];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) pr[r] = fast_exp2(__builtin_fmaf(sc[r], p.scale_log2, -ms));
+      float ls = 0.f;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) ls += pr[r];
+      l += ls;
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        f32x4_t a4 = {pr[8 * c], pr[8 * c + 1], pr[8 * c + 2], pr[8 * c + 3]};
+        f32x4_t b4 = {pr[8 * c + 4], pr[8 * c + 5], pr[8 * c + 6], pr[8 * c + 7]};
+        const uint2 ua = PMfma<T>::pack(a4), ub = PMfma<T>::pack(b4);
+        const uint4 pk = make_uint4(ua.x, ua.y, ub.x, ub.y);
+        // V^T of dim 32j + n, keys 16c + 4h .. +3 and 16c + 8 + 4h .. +3 of the step
+        const char* vs = st + L::KST + n * L::VRS + (32 * h2 + 16 * c + 4 * h) * 2;
+#pragma unroll
+        for (int j = 0; j < D / 32; ++j) {
+          const uint2 va = *(const uint2*)(vs + 32 * j * L::VRS);
+          const uint2 vb = *(const uint2*)(vs + 32 * j * L::VRS + 16);
+          o[j] = M::mma(make_uint4(va.x, va.y, vb.x, vb.y), pk, o[j]);
+        }
+      }
+    }
+    if (more) lstore(stage ^ 1);
+    __syncthreads();
+  }
+
+  // O^T value r of block j is dim 32j + 8(r/4) + 4h + r%4 of the lane's column.
+  const float lt = l + __shfl_xor(l, 32);
+  if (col_ok) {
+    const float inv = lt > 0.f ? 1.f / lt : 0.f;
+    S* ob = (S*)p.out + (((long)b * p.S + qpos) * p.Hq + qhead) * D + 4 * h;
+#pragma unroll
+    for (int j = 0; j < D / 32; ++j) {
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4) {
+        const uint32_t w0 = M::bits(o[j][4 * q4] * inv) | (M::bits(o[j][4 * q4 + 1] * inv) << 16);
+        const uint32_t w1 = M::bits(o[j][4 * q4 + 2] * inv) | (M::bits(o[j][4 * q4 + 3] * inv) << 16);
+        *(uint2*)(ob + 32 * j + 8 * q4) = make_uint2(w0, w1);
+      }
+    }
+  }
+}
+
+template <typename T, int G>
+int launch_prefill32(const PrefillParams& p, int batch, hipStream_t stream) {
+  const int blocks = (p.S * G + kP32Rows - 1) / kP32Rows;
+  hipLaunchKernelGGL((prefill_attn32_kernel<T, G>), dim3(blocks, p.Hkv, batch), dim3(kP32Threads), 0, stream, p);
+  return (int)hipGetLastError();
+}
+
 template <typename T, int D, int G>
 int launch_prefill(const PrefillParams& p, int batch, hipStream_t stream) {
-  const int blocks = (p.S * G + kPfRows - 1) / kPfRows;
-  hipLaunchKernelGGL((prefill_attn_kernel<T, D, G>), dim3(blocks, p.Hkv, batch), dim3(kPfThreads), 0, stream, p);
-  return (int)hipGetLastError();
+  if constexpr (D == 128) {
+    return launch_prefill32<T, G>(p, batch, stream);
+  } else {
+    const int blocks = (p.S * G + kPfRows - 1) / kPfRows;
+    hipLaunchKernelGGL((prefill_attn_kernel<T, D, G>), dim3(blocks, p.Hkv, batch), dim3(kPfThreads), 0, stream, p);
+    return (int)hipGetLastError();
+  }
 }
 
 template <typename T, int D>
