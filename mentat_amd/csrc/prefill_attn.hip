@@ -348,20 +348,18 @@ template <> struct PMfma32<F16> {
   __device__ static uint32_t bits(float v) { return f32_to_f16_bits(v); }
 };
 
-constexpr int kP32Waves = 4;
-constexpr int kP32Threads = 64 * kP32Waves;
-constexpr int kP32Rows = 32 * kP32Waves;  // query rows per workgroup
-
-template <typename T, int G>
-__global__ __launch_bounds__(kP32Threads) __attribute__((amdgpu_waves_per_eu(2, 2)))
+// W wavefronts per workgroup: 32 W query rows share each staged K/V stage.
+template <typename T, int G, int W>
+__global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void prefill_attn32_kernel(PrefillParams p) {
+  constexpr int kP32Rows = 32 * W;
   using S = typename T::storage;
   constexpr int D = 128;
   using L = PfLds<D>;
   using M = PMfma32<T>;
   constexpr int CH = D / 8;        // 16-byte chunks per token row
   constexpr int NQ = kPfKeys / 4;  // token quads per stage
-  static_assert(NQ * CH == kP32Threads, "one (token quad, chunk) per thread and stage");
+  static_assert(NQ * CH <= 64 * W, "one (token quad, chunk) per thread and stage");
   __shared__ __attribute__((aligned(16))) char lds[2 * L::STAGE];
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -402,9 +400,12 @@ void prefill_attn32_kernel(PrefillParams p) {
   for (int j = 0; j < D / 32; ++j) o[j] = f32x16_t{};
   float m = kNegInf, l = 0.f;
 
-  // Staging as in prefill_attn_kernel: thread tid moves tokens 4tq .. 4tq+3, dims
-  // 8lc .. 8lc+7 of K and V (V written transposed).
-  const int tq = tid / CH, lc = tid - (tid / CH) * CH;
+  // Staging as in prefill_attn_kernel: thread tid < NQ*CH moves tokens 4tq .. 4tq+3,
+  // dims 8lc .. 8lc+7 of K and V (V written transposed); the others load a copy and
+  // store nothing.
+  const bool loader = tid < NQ * CH;
+  const int lid = min(tid, NQ * CH - 1);
+  const int tq = lid / CH, lc = lid - (lid / CH) * CH;
   uint4 kw[4], vw[4];
   auto gload = [&](int t) {
 #pragma unroll
@@ -438,7 +439,7 @@ void prefill_attn32_kernel(PrefillParams p) {
   };
 
   gload(t_lo);
-  lstore(0);
+  if (loader) lstore(0);
   __syncthreads();
   for (int t = t_lo; t <= t_hi; ++t) {
     const int stage = (t - t_lo) & 1;
@@ -502,7 +503,7 @@ void prefill_attn32_kernel(PrefillParams p) {
         }
       }
     }
-    if (more) lstore(stage ^ 1);
+    if (loader && more) lstore(stage ^ 1);
     __syncthreads();
   }
 
@@ -523,11 +524,17 @@ void prefill_attn32_kernel(PrefillParams p) {
   }
 }
 
+template <typename T, int G, int W>
+int launch_prefill32w(const PrefillParams& p, int batch, hipStream_t stream) {
+  const int blocks = (p.S * G + 32 * W - 1) / (32 * W);
+  hipLaunchKernelGGL((prefill_attn32_kernel<T, G, W>), dim3(blocks, p.Hkv, batch), dim3(64 * W), 0, stream, p);
+  return (int)hipGetLastError();
+}
+// Four wavefronts (128 rows) per workgroup, two workgroups per CU: 424 TFLOP/s at
+// Llama-3-8B prefill shapes against 392 with eight (one workgroup per CU).
 template <typename T, int G>
 int launch_prefill32(const PrefillParams& p, int batch, hipStream_t stream) {
-  const int blocks = (p.S * G + kP32Rows - 1) / kP32Rows;
-  hipLaunchKernelGGL((prefill_attn32_kernel<T, G>), dim3(blocks, p.Hkv, batch), dim3(kP32Threads), 0, stream, p);
-  return (int)hipGetLastError();
+  return launch_prefill32w<T, G, 4>(p, batch, stream);
 }
 
 template <typename T, int D, int G>
