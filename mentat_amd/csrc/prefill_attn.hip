@@ -151,19 +151,23 @@ __global__ __launch_bounds__(kPfThreads) void prefill_attn_kernel(PrefillParams 
   // Staging: thread tid < NQ*CH moves tokens 4*tq .. 4*tq+3, dims 8*lc .. 8*lc+7 of
   // K and V; the other threads load a copy of the last block and store nothing,
   // so every load is issued outside any branch.
+  // (V with the token quad fastest over consecutive threads: see prefill_attn32_kernel.)
   const bool loader = tid < NQ * CH;
   const int lid = min(tid, NQ * CH - 1);
   const int tq = lid / CH, lc = lid - (lid / CH) * CH;
+  const int tqv = lid % NQ, lcv = lid / NQ;
   uint4 kw[4], vw[4];
   auto gload = [&](int t) {
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       const int tok = t * kPfKeys + 4 * tq + u;
       const int tc = min(tok, p.S - 1);
-      const long off = (((long)b * p.S + tc) * p.Hkv + hk) * D + 8 * lc;
-      kw[u] = *(const uint4*)((const S*)p.k + off);
-      vw[u] = *(const uint4*)((const S*)p.v + off);
-      if (tok >= p.S) { kw[u] = make_uint4(0, 0, 0, 0); vw[u] = make_uint4(0, 0, 0, 0); }
+      kw[u] = *(const uint4*)((const S*)p.k + (((long)b * p.S + tc) * p.Hkv + hk) * D + 8 * lc);
+      if (tok >= p.S) kw[u] = make_uint4(0, 0, 0, 0);
+      const int tokv = t * kPfKeys + 4 * tqv + u;
+      const int tcv = min(tokv, p.S - 1);
+      vw[u] = *(const uint4*)((const S*)p.v + (((long)b * p.S + tcv) * p.Hkv + hk) * D + 8 * lcv);
+      if (tokv >= p.S) vw[u] = make_uint4(0, 0, 0, 0);
     }
   };
   auto lstore = [&](int stage) {
@@ -175,7 +179,7 @@ __global__ __launch_bounds__(kPfThreads) void prefill_attn_kernel(PrefillParams 
     const uint32_t* w1 = (const uint32_t*)&vw[1];
     const uint32_t* w2 = (const uint32_t*)&vw[2];
     const uint32_t* w3 = (const uint32_t*)&vw[3];
-    char* vt = st + L::KST + 8 * tq;
+    char* vt = st + L::KST + 8 * tqv;
 #pragma unroll
     for (int h = 0; h < 4; ++h) {
       // dims 8lc + 2h (low halves) and 8lc + 2h + 1 (high halves)
@@ -183,8 +187,8 @@ __global__ __launch_bounds__(kPfThreads) void prefill_attn_kernel(PrefillParams 
                                   __builtin_amdgcn_perm(w3[h], w2[h], 0x05040100u));
       const uint2 hi = make_uint2(__builtin_amdgcn_perm(w1[h], w0[h], 0x07060302u),
                                   __builtin_amdgcn_perm(w3[h], w2[h], 0x07060302u));
-      *(uint2*)(vt + (8 * lc + 2 * h) * L::VRS) = lo;
-      *(uint2*)(vt + (8 * lc + 2 * h + 1) * L::VRS) = hi;
+      *(uint2*)(vt + (8 * lcv + 2 * h) * L::VRS) = lo;
+      *(uint2*)(vt + (8 * lcv + 2 * h + 1) * L::VRS) = hi;
     }
   };
 
@@ -403,19 +407,26 @@ void prefill_attn32_kernel(PrefillParams p) {
   // Staging as in prefill_attn_kernel: thread tid < NQ*CH moves tokens 4tq .. 4tq+3,
   // dims 8lc .. 8lc+7 of K and V (V written transposed); the others load a copy and
   // store nothing.
+  // K: chunk fastest over consecutive threads (coalesced loads, one K row per 16
+  // threads); V: token quad fastest, so that the 16 threads of a V^T write fill one
+  // contiguous row segment (chunk-fastest V^T writes are 8 rows apart and meet in
+  // two LDS banks).
   const bool loader = tid < NQ * CH;
   const int lid = min(tid, NQ * CH - 1);
   const int tq = lid / CH, lc = lid - (lid / CH) * CH;
+  const int tqv = lid % NQ, lcv = lid / NQ;
   uint4 kw[4], vw[4];
   auto gload = [&](int t) {
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       const int tok = t * kPfKeys + 4 * tq + u;
       const int tc = min(tok, p.S - 1);
-      const long off = (((long)b * p.S + tc) * p.Hkv + hk) * D + 8 * lc;
-      kw[u] = *(const uint4*)((const S*)p.k + off);
-      vw[u] = *(const uint4*)((const S*)p.v + off);
-      if (tok >= p.S) { kw[u] = make_uint4(0, 0, 0, 0); vw[u] = make_uint4(0, 0, 0, 0); }
+      kw[u] = *(const uint4*)((const S*)p.k + (((long)b * p.S + tc) * p.Hkv + hk) * D + 8 * lc);
+      if (tok >= p.S) kw[u] = make_uint4(0, 0, 0, 0);
+      const int tokv = t * kPfKeys + 4 * tqv + u;
+      const int tcv = min(tokv, p.S - 1);
+      vw[u] = *(const uint4*)((const S*)p.v + (((long)b * p.S + tcv) * p.Hkv + hk) * D + 8 * lcv);
+      if (tokv >= p.S) vw[u] = make_uint4(0, 0, 0, 0);
     }
   };
   auto lstore = [&](int stage) {
@@ -426,15 +437,15 @@ void prefill_attn32_kernel(PrefillParams p) {
     const uint32_t* w1 = (const uint32_t*)&vw[1];
     const uint32_t* w2 = (const uint32_t*)&vw[2];
     const uint32_t* w3 = (const uint32_t*)&vw[3];
-    char* vt = st + L::KST + 8 * tq;
+    char* vt = st + L::KST + 8 * tqv;
 #pragma unroll
     for (int hh = 0; hh < 4; ++hh) {
       const uint2 lo = make_uint2(__builtin_amdgcn_perm(w1[hh], w0[hh], 0x05040100u),
                                   __builtin_amdgcn_perm(w3[hh], w2[hh], 0x05040100u));
       const uint2 hi = make_uint2(__builtin_amdgcn_perm(w1[hh], w0[hh], 0x07060302u),
                                   __builtin_amdgcn_perm(w3[hh], w2[hh], 0x07060302u));
-      *(uint2*)(vt + (8 * lc + 2 * hh) * L::VRS) = lo;
-      *(uint2*)(vt + (8 * lc + 2 * hh + 1) * L::VRS) = hi;
+      *(uint2*)(vt + (8 * lcv + 2 * hh) * L::VRS) = lo;
+      *(uint2*)(vt + (8 * lcv + 2 * hh + 1) * L::VRS) = hi;
     }
   };
 
