@@ -416,17 +416,24 @@ void prefill_attn32_kernel(PrefillParams p) {
   const int tq = lid / CH, lc = lid - (lid / CH) * CH;
   const int tqv = lid % NQ, lcv = lid / NQ;
   uint4 kw[4], vw[4];
+  // Buffer loads over this (batch, kv head)'s rows: the stage's token offset rides in
+  // the scalar offset, the thread's part is fixed, and tokens past the sequence lie
+  // past the resource's end and read as zeros.
+  const long row_bytes = (long)p.Hkv * D * (long)sizeof(S);
+  const long head_off = (((long)b * p.S) * p.Hkv + hk) * D * (long)sizeof(S);
+  const int rs_bytes = (int)((long)(p.S - 1) * row_bytes + D * (long)sizeof(S));
+  const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<char*>((const char*)p.k + head_off), (short)0, rs_bytes, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<char*>((const char*)p.v + head_off), (short)0, rs_bytes, 0x00020000);
+  const int koff = (int)(4 * tq * row_bytes) + 16 * lc;
+  const int voff = (int)(4 * tqv * row_bytes) + 16 * lcv;
   auto gload = [&](int t) {
+    const int so = (int)((long)t * kPfKeys * row_bytes);  // within the resource or past its end
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-      const int tok = t * kPfKeys + 4 * tq + u;
-      const int tc = min(tok, p.S - 1);
-      kw[u] = *(const uint4*)((const S*)p.k + (((long)b * p.S + tc) * p.Hkv + hk) * D + 8 * lc);
-      if (tok >= p.S) kw[u] = make_uint4(0, 0, 0, 0);
-      const int tokv = t * kPfKeys + 4 * tqv + u;
-      const int tcv = min(tokv, p.S - 1);
-      vw[u] = *(const uint4*)((const S*)p.v + (((long)b * p.S + tcv) * p.Hkv + hk) * D + 8 * lcv);
-      if (tokv >= p.S) vw[u] = make_uint4(0, 0, 0, 0);
+      kw[u] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rk, koff + (int)(u * row_bytes), so, 0));
+      vw[u] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rv, voff + (int)(u * row_bytes), so, 0));
     }
   };
   auto lstore = [&](int stage) {
@@ -537,6 +544,8 @@ void prefill_attn32_kernel(PrefillParams p) {
 
 template <typename T, int G, int W>
 int launch_prefill32w(const PrefillParams& p, int batch, hipStream_t stream) {
+  // 32-bit buffer offsets over one (batch, kv head)'s rows, the last stage's included
+  if ((long)(p.S + kPfKeys) * p.Hkv * 128 * (long)sizeof(typename T::storage) > 0x7fffffffL) return MENTAT_EUNSUP;
   const int blocks = (p.S * G + 32 * W - 1) / (32 * W);
   hipLaunchKernelGGL((prefill_attn32_kernel<T, G, W>), dim3(blocks, p.Hkv, batch), dim3(64 * W), 0, stream, p);
   return (int)hipGetLastError();
