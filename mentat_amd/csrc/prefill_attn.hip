@@ -23,7 +23,9 @@
 // rides in the exponent's fma. One tile per wavefront, 8 wavefronts and
 // 64-key stages measured fastest (more tiles per wavefront raise register use
 // to one wavefront per SIMD; 4 wavefronts or 32-key stages re-stage K/V for
-// fewer rows; 128-key stages halve the resident workgroups).
+// fewer rows; 128-key stages halve the resident workgroups). That is the
+// head_dim 64 kernel; head_dim 128 runs prefill_attn32_kernel below (32
+// columns per wavefront on v_mfma_f32_32x32x16).
 //
 // fp32 prompts run on the VALU decode kernel instead (causal_prefill_f32 in
 // paged_decode.hip): one query per position over its visible keys.
