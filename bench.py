@@ -12,8 +12,8 @@ algorithmic bytes), the roofline fraction against MI355X's 8 TB/s, and the
 reference's CPU path timed beside it on the same inputs.
 
 With no --workload (or --workload all) the line also carries "workloads": the
-tree, rows and e2e results below, each with its own ms_per_step, value,
-roofline and cpu_baseline.
+tree, rows, prefill and e2e results below, each with its own ms_per_step,
+value, roofline and cpu_baseline.
 
 Single workloads (their own JSON line, same fields):
   --workload tree   prefix-tree decode at Qwen3-8B attention shapes: 4 trees
@@ -24,6 +24,8 @@ Single workloads (their own JSON line, same fields):
                     of 256 ids, 512 new tokens, absolute gate 2.5 nats, up to 8
                     branches per prompt, all prompts continuously batched
                     (branch-decode tokens/s)
+  --workload prefill  causal GQA prefill attention, 4 prompts x 2048 positions,
+                    Llama-3-8B heads, bf16 (TFLOP/s against the dense bf16 peak)
 
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload all|decode|tree|rows|e2e|prefill]
 """
@@ -602,13 +604,14 @@ def _summary(line: dict) -> dict:
 def run_all(args, dev) -> dict:
     """The headline (paged decode at Llama-3-8B shapes) with the other measured
     workloads nested under "workloads": prefix-tree decode, the fused entropy
-    gate + sampling step and the end-to-end rollout (branch-decode tokens/s).
+    gate + sampling step, prefill attention and the end-to-end rollout
+    (branch-decode tokens/s).
     A workload that fails is reported with its error instead of its numbers."""
     import torch
 
     line = run_decode(args, dev)
     nested = {}
-    for name, fn in (("tree", run_tree), ("rows", run_rows), ("e2e", run_e2e)):
+    for name, fn in (("tree", run_tree), ("rows", run_rows), ("prefill", run_prefill), ("e2e", run_e2e)):
         torch.cuda.empty_cache()
         t0 = time.perf_counter()
         try:
@@ -628,7 +631,8 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", choices=("all", "decode", "tree", "rows", "e2e", "prefill"), default="all",
-                    help="all (default): the paged-decode headline plus tree, rows and e2e nested in one line")
+                    help="all (default): the paged-decode headline plus tree, rows, prefill and e2e nested "
+                         "in one line")
     ap.add_argument("--e2e-new-tokens", type=int, default=512)
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="minimum host time spent on the CPU baseline")
