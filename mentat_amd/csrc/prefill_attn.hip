@@ -544,10 +544,14 @@ void prefill_attn32_kernel(PrefillParams p) {
   }
 }
 
+// 32-bit buffer offsets over one (batch, kv head)'s rows, the last stage's included.
+template <typename T>
+bool prefill32_fits(const PrefillParams& p) {
+  return (long)(p.S + kPfKeys) * p.Hkv * 128 * (long)sizeof(typename T::storage) <= 0x7fffffffL;
+}
+
 template <typename T, int G, int W>
 int launch_prefill32w(const PrefillParams& p, int batch, hipStream_t stream) {
-  // 32-bit buffer offsets over one (batch, kv head)'s rows, the last stage's included
-  if ((long)(p.S + kPfKeys) * p.Hkv * 128 * (long)sizeof(typename T::storage) > 0x7fffffffL) return MENTAT_EUNSUP;
   const int blocks = (p.S * G + 32 * W - 1) / (32 * W);
   hipLaunchKernelGGL((prefill_attn32_kernel<T, G, W>), dim3(blocks, p.Hkv, batch), dim3(64 * W), 0, stream, p);
   return (int)hipGetLastError();
@@ -562,12 +566,12 @@ int launch_prefill32(const PrefillParams& p, int batch, hipStream_t stream) {
 template <typename T, int D, int G>
 int launch_prefill(const PrefillParams& p, int batch, hipStream_t stream) {
   if constexpr (D == 128) {
-    return launch_prefill32<T, G>(p, batch, stream);
-  } else {
-    const int blocks = (p.S * G + kPfRows - 1) / kPfRows;
-    hipLaunchKernelGGL((prefill_attn_kernel<T, D, G>), dim3(blocks, p.Hkv, batch), dim3(kPfThreads), 0, stream, p);
-    return (int)hipGetLastError();
+    if (prefill32_fits<T>(p)) return launch_prefill32<T, G>(p, batch, stream);
   }
+  // head_dim 64, or rows too long for 32-bit offsets: the 16-column kernel (64-bit addressing)
+  const int blocks = (p.S * G + kPfRows - 1) / kPfRows;
+  hipLaunchKernelGGL((prefill_attn_kernel<T, D, G>), dim3(blocks, p.Hkv, batch), dim3(kPfThreads), 0, stream, p);
+  return (int)hipGetLastError();
 }
 
 template <typename T, int D>
