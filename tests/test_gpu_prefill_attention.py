@@ -46,6 +46,11 @@ CASES = [
     (1, 90, 32, 8, 128, 1),
     (1, 50, 32, 8, 128, 4096),
     (1, 1000, 32, 8, 128, None),
+    # head_dim 128 (the 32-column kernel): 8 and 16 query heads per kv head, and a
+    # window spanning several 64-key stages
+    (1, 700, 32, 4, 128, 300),
+    (1, 129, 16, 1, 128, None),
+    (2, 450, 32, 8, 128, 190),
 ]
 
 
