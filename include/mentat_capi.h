@@ -272,6 +272,15 @@ int mentat_semantic_similar(const int64_t* ptrs, const int32_t* parent_key, cons
  * separate tensors, 2F for the halves of a merged gate/up projection), out
  * dense [rows][F], 16-byte aligned; silu(g) = g / (1 + exp(-g)) in fp32 (the
  * LlamaMLP / Qwen3MLP activation and product).
+ *
+ * mentat_silu_mul_split: the same product written as `split` column slices
+ * [split][rows][F / split] (F % (8 * split) == 0), the operand layout of a
+ * split-K down projection computed as one batched product over the slices.
+ *
+ * mentat_rmsnorm_partials: mentat_rmsnorm with x given as n_parts (2, 4 or 8)
+ * fp32 partial products parts[s][rows][H]: x = rnd(sum over s of parts[s]),
+ * the value one un-split down projection would have stored (up to the fp32
+ * summation order), then the residual add and the norm as above.
  * ------------------------------------------------------------------------ */
 int mentat_rmsnorm(const void* x, const void* residual_in, void* residual_out, const void* weight, void* out,
                    int rows, int H, float eps, int dtype, void* stream);
@@ -284,6 +293,12 @@ int mentat_rope_qkv(const void* qkv, int64_t row_stride, void* q, void* k, void*
 
 int mentat_silu_mul(const void* gate, const void* up, void* out, int rows, int F, int64_t in_row_stride, int dtype,
                     void* stream);
+
+int mentat_silu_mul_split(const void* gate, const void* up, void* out, int rows, int F, int64_t in_row_stride,
+                          int split, int dtype, void* stream);
+
+int mentat_rmsnorm_partials(const float* parts, int n_parts, const void* residual_in, void* residual_out,
+                            const void* weight, void* out, int rows, int H, float eps, int dtype, void* stream);
 
 /* ------------------------------------------------------------------------
  * KV append: write n new token rows into the pools, fused with the lazy

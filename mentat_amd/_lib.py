@@ -125,6 +125,16 @@ SIGNATURES: dict[str, tuple] = {
         ],
     ),
     "mentat_silu_mul": (_c_int, [_c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, _c_i64, _c_int, _c_void_p]),
+    "mentat_silu_mul_split": (
+        _c_int, [_c_void_p, _c_void_p, _c_void_p, _c_int, _c_int, _c_i64, _c_int, _c_int, _c_void_p],
+    ),
+    "mentat_rmsnorm_partials": (
+        _c_int,
+        [
+            _c_void_p, _c_int, _c_void_p, _c_void_p, _c_void_p, _c_void_p,  # parts, n_parts, res_in, res_out, w, out
+            _c_int, _c_int, _c_float, _c_int, _c_void_p,  # rows, H, eps, dtype, stream
+        ],
+    ),
     "mentat_semantic_ema": (
         _c_int,
         [

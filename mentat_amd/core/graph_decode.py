@@ -135,6 +135,31 @@ def _mergeable(a) -> bool:
 # captured again). "off": separate q/k/v and gate/up GEMMs.
 MERGE_PROJECTIONS = "copy"
 
+# "copy" mode also runs each layer's down projection split over the reduction:
+# its weight is copied as SPLIT_DOWN column slices [S, F/S, H], the activation
+# is written as the matching slices [S, nb, F/S], one batched product gives S
+# fp32 partials [S, nb, H], and the next RMSNorm sums them and rounds once to
+# the dtype (the value the un-split product stores, up to the fp32 summation
+# order). At decode row counts the single [nb, F] x [F, H] product has too few
+# output tiles to fill the device; S slices give S times as many. 0 or 1: off.
+SPLIT_DOWN = 8
+
+
+def _project(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+    """The step's product of rows x with a projection weight: linear for an
+    [out, in] weight; for split slices w [S, F/S, H], x [rows, F/S] is taken
+    as every slice's rows (the shape and cost of the split product)."""
+    if w.dim() == 3:
+        return torch.bmm(x.unsqueeze(0).expand(w.shape[0], -1, -1).contiguous(), w, out_dtype=torch.float32)
+    return torch.nn.functional.linear(x, w)
+
+
+def _split_copy(w: torch.Tensor, t: torch.Tensor) -> None:
+    """w [S, F/S, H] = the linear weight t [H, F] as S slices of its transpose:
+    w[s, f, h] = t[h, s * F/S + f]."""
+    S, Fs, H = w.shape
+    w.copy_(t.view(H, S, Fs).permute(1, 2, 0))
+
 
 def _merge_linears(lins) -> torch.Tensor:
     """One weight [sum(out), in] for the bias-free linears ``lins``; each
@@ -203,6 +228,7 @@ class DecodeGraphs:
         self._w_qkv: list = []
         self._w_gu: list = []
         self._w_src: list = []   # "copy": per layer [module params dict, tensor, data_ptr, version, merged, row]
+        self._w_down: list = []  # "copy" with SPLIT_DOWN > 1: per layer down weight as [S, F/S, H]
         if self.merged:
             self._merge()
         Hq, Hkv = self.a.num_attention_heads, self.a.num_key_value_heads
@@ -225,13 +251,14 @@ class DecodeGraphs:
     def _projection_weights(self) -> list:
         """The weights of the step's projection GEMMs, in step order: per layer
         q/k/v (merged when the step merges them), o, gate/up (likewise) and
-        down, then the LM head."""
+        down (its [S, F/S, H] slices when the step splits it), then the LM head."""
         a = self.a
         mats = []
         for i, b in enumerate(a.layers):
             attn, mlp = a.get_self_attn(b), a.get_mlp(b)
             if self.merged:
-                mats += [self._w_qkv[i], attn.o_proj.weight, self._w_gu[i], mlp.down_proj.weight]
+                down = self._w_down[i] if self._w_down else mlp.down_proj.weight
+                mats += [self._w_qkv[i], attn.o_proj.weight, self._w_gu[i], down]
             else:
                 mats += [attn.q_proj.weight, attn.k_proj.weight, attn.v_proj.weight, attn.o_proj.weight,
                          mlp.gate_proj.weight, mlp.up_proj.weight, mlp.down_proj.weight]
@@ -247,7 +274,7 @@ class DecodeGraphs:
             key = (tuple(w.shape), w.dtype)
             if key not in seen:
                 seen.add(key)
-                torch.nn.functional.linear(torch.zeros(nb, w.shape[1], dtype=w.dtype, device=self.dev), w)
+                _project(torch.zeros(nb, w.shape[-2 if w.dim() == 3 else 1], dtype=w.dtype, device=self.dev), w)
 
     @torch.no_grad()
     def calibrate_buckets(self, max_batch: int = 256, step: int = 8, reps: int = 3, tol: float = 0.01) -> tuple:
@@ -265,12 +292,13 @@ class DecodeGraphs:
         g = torch.Generator(device=self.dev).manual_seed(0)
         xs = {}
         for w in mats:
-            if w.shape[1] not in xs:
-                xs[w.shape[1]] = torch.randn(max_batch, w.shape[1], generator=g, device=self.dev).to(w.dtype)
+            k = w.shape[-2] if w.dim() == 3 else w.shape[1]
+            if k not in xs:
+                xs[k] = torch.randn(max_batch, k, generator=g, device=self.dev).to(w.dtype)
 
         def projections(r):
             for w in mats:
-                torch.nn.functional.linear(xs[w.shape[1]][:r], w)
+                _project(xs[w.shape[-2] if w.dim() == 3 else w.shape[1]][:r], w)
 
         cost = {}
         for r in range(step, max_batch + 1, step):
@@ -295,9 +323,19 @@ class DecodeGraphs:
                 self._w_qkv = [_merge_linears(groups(b)[0]) for b in self.a.layers]
                 self._w_gu = [_merge_linears(groups(b)[1]) for b in self.a.layers]
                 return
-            self._w_qkv, self._w_gu, self._w_src = [], [], []
+            self._w_qkv, self._w_gu, self._w_src, self._w_down = [], [], [], []
+            S = SPLIT_DOWN
+            split = S > 1 and all(
+                isinstance(b.mlp.down_proj, torch.nn.Linear) and b.mlp.down_proj.bias is None
+                and b.mlp.down_proj.weight.shape[1] % (8 * S) == 0 for b in self.a.layers)
             for b in self.a.layers:
                 recs = []
+                if split:
+                    t = b.mlp.down_proj._parameters["weight"]
+                    w = torch.empty(S, t.shape[1] // S, t.shape[0], dtype=t.dtype, device=t.device)
+                    _split_copy(w, t.detach())
+                    self._w_down.append(w)
+                    recs.append([b.mlp.down_proj._parameters, t, t.data_ptr(), t._version, w, None])
                 for lins, dst in zip(groups(b), (self._w_qkv, self._w_gu)):
                     w = torch.cat([lin.weight.detach() for lin in lins], dim=0)
                     dst.append(w)
@@ -335,6 +373,13 @@ class DecodeGraphs:
                 if t is r[1] and t._version == r[3] and t.data_ptr() == r[2]:
                     continue
                 w, row = r[4], r[5]
+                if row is None:   # a split down projection weight
+                    if t.shape != r[1].shape or t.dtype != w.dtype:
+                        raise ValueError("DecodeGraphs: a split projection weight changed shape or dtype")
+                    with torch.no_grad():
+                        _split_copy(w, t.detach())
+                    r[1], r[2], r[3] = t, t.data_ptr(), t._version
+                    continue
                 if t.shape[0] != r[1].shape[0] or t.shape[1:] != w.shape[1:] or t.dtype != w.dtype:
                     raise ValueError("DecodeGraphs: a merged projection weight changed shape or dtype")
                 with torch.no_grad():
@@ -475,6 +520,16 @@ class DecodeGraphs:
             ln = block.post_attention_layernorm
             x, hidden = ops.rmsnorm(attn_out, ln.weight, ln.variance_epsilon, residual=hidden)
             mlp = block.mlp
+            if self._w_down:
+                gu = torch.nn.functional.linear(x, self._w_gu[layer_idx])
+                w_down = self._w_down[layer_idx]
+                act = ops.silu_mul_merged_split(gu.view(nb, -1), w_down.shape[0])  # [S, nb, F/S]
+                parts = torch.bmm(act, w_down, out_dtype=torch.float32)           # [S, nb, H]
+                ln = layers[layer_idx + 1].input_layernorm if layer_idx + 1 < L else a.final_norm
+                x, hidden = ops.rmsnorm_partials(parts, ln.weight, ln.variance_epsilon,
+                                                 residual=hidden.view(nb, -1))
+                x, hidden = x.view(1, nb, -1), hidden.view(1, nb, -1)
+                continue
             if self.merged:
                 act = ops.silu_mul_merged(torch.nn.functional.linear(x, self._w_gu[layer_idx]))
             else:

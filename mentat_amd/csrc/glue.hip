@@ -26,11 +26,15 @@ constexpr int kNormThreads = 256;
 // thread owns NG groups (H a multiple of 2048), so no load sits under a branch.
 // The weight is loaded with the row, before the block reduction, so the row
 // costs one memory round trip.
+// NP > 0: x is not given; each element is the sum of NP fp32 partials (xp + s *
+// pstride, the slices of a split-K product) rounded once to the dtype, the value a
+// single product would have stored.
 constexpr int kNormGroups = 4;
-template <typename T, int NG, bool FULL>
+template <typename T, int NG, bool FULL, int NP = 0>
 __global__ __launch_bounds__(kNormThreads) void rmsnorm_kernel(const uint16_t* x, const uint16_t* res_in,
                                                                uint16_t* res_out, const uint16_t* w, uint16_t* y,
-                                                               int H, float eps) {
+                                                               int H, float eps, const float* xp = nullptr,
+                                                               long pstride = 0) {
   using E = G16<T>;
   const int row = blockIdx.x, tid = threadIdx.x;
   const long base = (long)row * H;
@@ -42,7 +46,25 @@ __global__ __launch_bounds__(kNormThreads) void rmsnorm_kernel(const uint16_t* x
   for (int k = 0; k < NG; ++k) {
     const int g = tid + k * kNormThreads;
     if (FULL || g < ng) {
-      const uint4 xv = *(const uint4*)(x + base + 8 * g);
+      uint4 xv;
+      if constexpr (NP > 0) {
+        float4 pa[NP], pb[NP];
+#pragma unroll
+        for (int q = 0; q < NP; ++q) {
+          pa[q] = *(const float4*)(xp + q * pstride + base + 8 * g);
+          pb[q] = *(const float4*)(xp + q * pstride + base + 8 * g + 4);
+        }
+        float a8[8] = {pa[0].x, pa[0].y, pa[0].z, pa[0].w, pb[0].x, pb[0].y, pb[0].z, pb[0].w};
+#pragma unroll
+        for (int q = 1; q < NP; ++q) {
+          a8[0] += pa[q].x; a8[1] += pa[q].y; a8[2] += pa[q].z; a8[3] += pa[q].w;
+          a8[4] += pb[q].x; a8[5] += pb[q].y; a8[6] += pb[q].z; a8[7] += pb[q].w;
+        }
+        xv = make_uint4(E::bits(a8[0]) | (E::bits(a8[1]) << 16), E::bits(a8[2]) | (E::bits(a8[3]) << 16),
+                        E::bits(a8[4]) | (E::bits(a8[5]) << 16), E::bits(a8[6]) | (E::bits(a8[7]) << 16));
+      } else {
+        xv = *(const uint4*)(x + base + 8 * g);
+      }
       wv[k] = *(const uint4*)(w + 8 * g);
       const uint32_t xs[4] = {xv.x, xv.y, xv.z, xv.w};
       if (res_in) {
@@ -160,13 +182,22 @@ __global__ __launch_bounds__(256) void rope_kernel(const uint16_t* qi, uint16_t*
 
 // m[r][j] = rnd(rnd(silu(g[r][j])) * u[r][j]) for rows r and j < F (F % 8 == 0): g and u rows
 // in_stride elements apart, m dense; 8 elements per thread, grid ceil(rows * F / 8 / 256).
+// With split = S > 1, m is [S][rows][F / S] instead (column j of row r at
+// ((j / (F/S)) * rows + r) * (F/S) + j % (F/S)): the K slices of a split-K
+// product with the next projection, each slice dense.
 template <typename T>
 __global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t* g, const uint16_t* u, uint16_t* m, long n8,
-                                                       int F8, long in_stride) {
+                                                       int F8, long in_stride, long rows, int split) {
   using E = G16<T>;
   const long i = (long)blockIdx.x * 256 + threadIdx.x;
   if (i >= n8) return;
   const long r = i / F8, c = i - r * F8;
+  long mo = 8 * i;
+  if (split > 1) {
+    const int fs8 = F8 / split;
+    const long sl = c / fs8;
+    mo = 8 * ((sl * rows + r) * fs8 + (c - sl * fs8));
+  }
   const long io = r * in_stride + 8 * c;
   const uint4 gv = *(const uint4*)(g + io), uv = *(const uint4*)(u + io);
   const uint32_t gs[4] = {gv.x, gv.y, gv.z, gv.w}, us[4] = {uv.x, uv.y, uv.z, uv.w};
@@ -178,7 +209,7 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t* g, const 
     const float b = E::rnd(E::rnd(g1 / (1.f + expf(-g1))) * E::hi(us[j]));
     o[j] = E::bits(a) | (E::bits(b) << 16);
   }
-  *(uint4*)(m + 8 * i) = make_uint4(o[0], o[1], o[2], o[3]);
+  *(uint4*)(m + mo) = make_uint4(o[0], o[1], o[2], o[3]);
 }
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
@@ -214,6 +245,63 @@ extern "C" int mentat_rmsnorm(const void* x, const void* residual_in, void* resi
     default:
       return MENTAT_EUNSUP;
   }
+  return (int)hipGetLastError();
+}
+
+template <typename T, int NP>
+static void launch_rmsnorm_parts(int rows, int H, hipStream_t s, const float* xp, const uint16_t* ri, uint16_t* ro,
+                                 const uint16_t* wi, uint16_t* yo, float eps) {
+  const long ps = (long)rows * H;
+  switch ((H / 8 + kNormThreads - 1) / kNormThreads) {
+#define MENTAT_NORM_PARTS(NGV)                                                                                   \
+  if ((H / 8) % kNormThreads == 0)                                                                               \
+    hipLaunchKernelGGL((rmsnorm_kernel<T, NGV, true, NP>), dim3(rows), dim3(kNormThreads), 0, s, nullptr, ri, ro, \
+                       wi, yo, H, eps, xp, ps);                                                                  \
+  else                                                                                                           \
+    hipLaunchKernelGGL((rmsnorm_kernel<T, NGV, false, NP>), dim3(rows), dim3(kNormThreads), 0, s, nullptr, ri, ro, \
+                       wi, yo, H, eps, xp, ps);
+    case 1: MENTAT_NORM_PARTS(1) break;
+    case 2: MENTAT_NORM_PARTS(2) break;
+    case 3: MENTAT_NORM_PARTS(3) break;
+    default: MENTAT_NORM_PARTS(4) break;
+#undef MENTAT_NORM_PARTS
+  }
+}
+
+template <typename T>
+static int rmsnorm_parts_t(int n_parts, int rows, int H, hipStream_t s, const float* xp, const uint16_t* ri,
+                           uint16_t* ro, const uint16_t* wi, uint16_t* yo, float eps) {
+  switch (n_parts) {
+    case 2: launch_rmsnorm_parts<T, 2>(rows, H, s, xp, ri, ro, wi, yo, eps); break;
+    case 4: launch_rmsnorm_parts<T, 4>(rows, H, s, xp, ri, ro, wi, yo, eps); break;
+    case 8: launch_rmsnorm_parts<T, 8>(rows, H, s, xp, ri, ro, wi, yo, eps); break;
+    default: return MENTAT_EUNSUP;
+  }
+  return MENTAT_OK;
+}
+
+extern "C" int mentat_rmsnorm_partials(const float* parts, int n_parts, const void* residual_in, void* residual_out,
+                                       const void* weight, void* out, int rows, int H, float eps, int dtype,
+                                       void* stream) {
+  if (rows < 0 || H <= 0 || n_parts < 1) return MENTAT_EINVAL;
+  if (rows == 0) return MENTAT_OK;
+  if (!parts || !weight || !out || (residual_in && !residual_out)) return MENTAT_EINVAL;
+  if (H % 8 != 0 || H > 8 * kNormThreads * kNormGroups) return MENTAT_EUNSUP;
+  if (!aligned16(parts) || !aligned16(weight) || !aligned16(out) ||
+      (residual_in && (!aligned16(residual_in) || !aligned16(residual_out))))
+    return MENTAT_EINVAL;
+  hipStream_t s = (hipStream_t)stream;
+  const auto* ri = (const uint16_t*)residual_in;
+  auto* ro = (uint16_t*)residual_out;
+  const auto* wi = (const uint16_t*)weight;
+  auto* yo = (uint16_t*)out;
+  int st;
+  switch (dtype) {
+    case MENTAT_BF16: st = rmsnorm_parts_t<BF16>(n_parts, rows, H, s, parts, ri, ro, wi, yo, eps); break;
+    case MENTAT_F16: st = rmsnorm_parts_t<F16>(n_parts, rows, H, s, parts, ri, ro, wi, yo, eps); break;
+    default: return MENTAT_EUNSUP;
+  }
+  if (st != MENTAT_OK) return st;
   return (int)hipGetLastError();
 }
 
@@ -275,11 +363,36 @@ extern "C" int mentat_silu_mul(const void* gate, const void* up, void* out, int 
   switch (dtype) {
     case MENTAT_BF16:
       hipLaunchKernelGGL(silu_mul_kernel<BF16>, grid, dim3(256), 0, s, (const uint16_t*)gate, (const uint16_t*)up,
-                         (uint16_t*)out, n8, F / 8, (long)in_row_stride);
+                         (uint16_t*)out, n8, F / 8, (long)in_row_stride, (long)rows, 1);
       break;
     case MENTAT_F16:
       hipLaunchKernelGGL(silu_mul_kernel<F16>, grid, dim3(256), 0, s, (const uint16_t*)gate, (const uint16_t*)up,
-                         (uint16_t*)out, n8, F / 8, (long)in_row_stride);
+                         (uint16_t*)out, n8, F / 8, (long)in_row_stride, (long)rows, 1);
+      break;
+    default:
+      return MENTAT_EUNSUP;
+  }
+  return (int)hipGetLastError();
+}
+
+extern "C" int mentat_silu_mul_split(const void* gate, const void* up, void* out, int rows, int F, int64_t in_row_stride,
+                                     int split, int dtype, void* stream) {
+  if (rows < 0 || F < 0 || in_row_stride < F || split < 1) return MENTAT_EINVAL;
+  if (rows == 0 || F == 0) return MENTAT_OK;
+  if (!gate || !up || !out) return MENTAT_EINVAL;
+  if (F % (8 * split) != 0 || in_row_stride % 8 != 0 || !aligned16(gate) || !aligned16(up) || !aligned16(out))
+    return MENTAT_EUNSUP;
+  hipStream_t s = (hipStream_t)stream;
+  const long n8 = (long)rows * (F / 8);
+  const dim3 grid((unsigned)((n8 + 255) / 256));
+  switch (dtype) {
+    case MENTAT_BF16:
+      hipLaunchKernelGGL(silu_mul_kernel<BF16>, grid, dim3(256), 0, s, (const uint16_t*)gate, (const uint16_t*)up,
+                         (uint16_t*)out, n8, F / 8, (long)in_row_stride, (long)rows, split);
+      break;
+    case MENTAT_F16:
+      hipLaunchKernelGGL(silu_mul_kernel<F16>, grid, dim3(256), 0, s, (const uint16_t*)gate, (const uint16_t*)up,
+                         (uint16_t*)out, n8, F / 8, (long)in_row_stride, (long)rows, split);
       break;
     default:
       return MENTAT_EUNSUP;

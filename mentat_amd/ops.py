@@ -391,6 +391,45 @@ def silu_mul_merged(gu: torch.Tensor) -> torch.Tensor:
     return out
 
 
+def silu_mul_merged_split(gu: torch.Tensor, split: int) -> torch.Tensor:
+    """silu_mul_merged of a [rows, 2F] projection output, returned as the
+    column slices [split, rows, F / split] that a split-K down projection
+    takes as its batched left operand (mentat_silu_mul_split)."""
+    _require(gu.dtype in _GLUE_DTYPES and gu.is_contiguous() and gu.dim() == 2 and gu.shape[-1] % 2 == 0,
+             "silu_mul_merged_split takes a contiguous bf16/f16 [rows, 2F] tensor")
+    F = gu.shape[-1] // 2
+    rows = gu.shape[0]
+    _require(split >= 1 and F % (8 * split) == 0, "F must split into slices of a multiple of 8")
+    out = torch.empty(split, rows, F // split, dtype=gu.dtype, device=gu.device)
+    st = get_lib().mentat_silu_mul_split(ptr(gu), gu.data_ptr() + F * gu.element_size(), ptr(out), rows, F, 2 * F,
+                                         split, DTYPE_CODES[gu.dtype], stream_handle(gu.device))
+    check(st, "mentat_silu_mul_split")
+    return out
+
+
+def rmsnorm_partials(parts: torch.Tensor, weight: torch.Tensor, eps: float,
+                     residual: Optional[torch.Tensor] = None):
+    """rmsnorm of x = the sum of the fp32 partial products ``parts``
+    [S, rows, H] (S in 2, 4, 8) rounded once to weight's dtype, with the
+    residual add fused in as in rmsnorm. Returns ``(out, h)``
+    (mentat_rmsnorm_partials)."""
+    _require(parts.dtype == torch.float32 and parts.is_contiguous() and parts.dim() == 3,
+             "rmsnorm_partials takes contiguous fp32 partials [S, rows, H]")
+    _require(weight.dtype in _GLUE_DTYPES and weight.is_contiguous() and weight.dim() == 1
+             and weight.numel() == parts.shape[2], "weight must be a bf16/f16 vector of length H")
+    S, rows, H = parts.shape
+    out = torch.empty(rows, H, dtype=weight.dtype, device=parts.device)
+    h = None
+    if residual is not None:
+        _require(residual.shape == (rows, H) and residual.dtype == weight.dtype and residual.is_contiguous(),
+                 "residual must be [rows, H] of weight's dtype")
+        h = torch.empty_like(residual)
+    st = get_lib().mentat_rmsnorm_partials(ptr(parts), S, ptr(residual), ptr(h), ptr(weight), ptr(out), rows, H,
+                                           float(eps), DTYPE_CODES[weight.dtype], stream_handle(parts.device))
+    check(st, "mentat_rmsnorm_partials")
+    return out, h
+
+
 def semantic_ema(vectors: list, hidden: torch.Tensor, fresh: list, alpha: float) -> None:
     """Fold row i of ``hidden`` [n, H] into ``vectors[i]`` (an H-element
     contiguous tensor on the same device, updated in place): copied when

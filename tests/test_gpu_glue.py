@@ -134,3 +134,53 @@ def test_captured_step_fuses_the_glue(gpu):
     from mentat_amd.core.graph_decode import _mergeable
 
     assert _mergeable(get_adapter(model))
+
+
+@pytest.mark.parametrize("split", [2, 4, 8])
+@pytest.mark.parametrize("rows,F", [(41, 14336), (1, 64), (176, 1024)])
+def test_silu_mul_split_is_the_column_slices(gpu, split, rows, F):
+    print(f"case silu_mul_split S={split} rows={rows} F={F}", flush=True)
+    g = torch.Generator(device=gpu).manual_seed(rows + F + split)
+    gu = (3 * torch.randn(rows, 2 * F, generator=g, device=gpu)).to(torch.bfloat16)
+    out = ops.silu_mul_merged_split(gu, split)
+    ref = ops.silu_mul_merged(gu).view(rows, split, F // split).permute(1, 0, 2)
+    assert out.shape == (split, rows, F // split)
+    assert torch.equal(out, ref)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("S,rows,H", [(4, 152, 4096), (2, 1, 4096), (8, 7, 2048), (4, 33, 5120), (4, 3, 8)])
+def test_rmsnorm_partials_is_rmsnorm_of_the_rounded_sum(gpu, dtype, S, rows, H):
+    """The partials are summed in slice order in fp32 and rounded once; from
+    there the residual add and the norm are rmsnorm's, bit for bit."""
+    print(f"case rmsnorm_partials {dtype} S={S} rows={rows} H={H}", flush=True)
+    g = torch.Generator(device=gpu).manual_seed(S * 1000 + rows + H)
+    parts = torch.randn(S, rows, H, generator=g, device=gpu)
+    w = (1 + 0.2 * torch.randn(H, generator=g, device=gpu)).to(dtype)
+    res = torch.randn(rows, H, generator=g, device=gpu).to(dtype)
+    x = parts[0].clone()
+    for s in range(1, S):
+        x = x + parts[s]
+    x = x.to(dtype)
+    for residual in (None, res):
+        y_ref, h_ref = ops.rmsnorm(x, w, 1e-5, residual=residual)
+        y, h = ops.rmsnorm_partials(parts, w, 1e-5, residual=residual)
+        assert torch.equal(y, y_ref)
+        assert (h is None) == (residual is None)
+        if residual is not None:
+            assert torch.equal(h, h_ref)
+
+
+def test_split_down_projection_refreshes_and_matches(gpu):
+    """The split copy of a down weight is its transpose in column slices, and
+    an in-place change of the module's weight reaches the copy."""
+    from mentat_amd.core.graph_decode import _split_copy
+
+    g = torch.Generator(device=gpu).manual_seed(9)
+    W = torch.randn(256, 1024, generator=g, device=gpu).to(torch.bfloat16)
+    w = torch.empty(4, 256, 256, dtype=torch.bfloat16, device=gpu)
+    _split_copy(w, W)
+    act = torch.randn(5, 1024, generator=g, device=gpu).to(torch.bfloat16)
+    parts = torch.bmm(act.view(5, 4, 256).permute(1, 0, 2).contiguous(), w, out_dtype=torch.float32)
+    ref = act.float() @ W.float().t()
+    assert float((parts.sum(0) - ref).abs().max()) < 1e-2 * float(ref.abs().max())

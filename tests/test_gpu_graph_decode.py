@@ -250,7 +250,8 @@ def test_merged_projections_leave_the_model_alone_and_follow_its_weights(gpu):
     copies of the modules' weights: the modules keep their tensors, and a weight
     rebound (a new tensor) or changed in place is picked up by the next step,
     whose logits follow the new weights (no recapture: the copies are refreshed
-    in place)."""
+    in place). The down projection runs split over its reduction from its own
+    sliced copy, refreshed the same way."""
     print("case merged projections after a weight rebind and an in-place change", flush=True)
     model = _bf16_model()
     before = [(b.self_attn.q_proj.weight.data_ptr(), b.mlp.up_proj.weight.data_ptr()) for b in model.model.layers]
@@ -264,18 +265,20 @@ def test_merged_projections_leave_the_model_alone_and_follow_its_weights(gpu):
         wg.prefill(ids, sg)
         le, _ = we.decode_batch_tensor([7], [se])
         lg, _ = wg.decode_batch_tensor([7], [sg])
-        assert wg.graphs.merged
+        assert wg.graphs.merged and len(wg.graphs._w_down) == len(model.model.layers)
         assert float((lg.float() - le.float()).abs().max()) <= 2e-2 * float(le.float().abs().max()) + 2e-2
         n0 = wg.graphs.captures
         for b in model.model.layers:  # new tensors, new values
             b.self_attn.q_proj.weight.data = (b.self_attn.q_proj.weight.data * 1.5).clone()
             b.mlp.gate_proj.weight.data = (b.mlp.gate_proj.weight.data * 0.5).clone()
+            b.mlp.down_proj.weight.data = (b.mlp.down_proj.weight.data * 1.25).clone()
         le, _ = we.decode_batch_tensor([8], [se])
         lg, _ = wg.decode_batch_tensor([8], [sg])
         assert float((lg.float() - le.float()).abs().max()) <= 2e-2 * float(le.float().abs().max()) + 2e-2
         for b in model.model.layers:  # in place, the same tensors
             b.self_attn.v_proj.weight.mul_(-1.0)
             b.mlp.up_proj.weight.mul_(0.75)
+            b.mlp.down_proj.weight.mul_(-0.5)
         le, _ = we.decode_batch_tensor([9], [se])
         lg, _ = wg.decode_batch_tensor([9], [sg])
         assert float((lg.float() - le.float()).abs().max()) <= 2e-2 * float(le.float().abs().max()) + 2e-2
